@@ -1,0 +1,272 @@
+"""numpy front end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the CPU baseline. Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+package; the product (raggedroute_amd) never does. Each function wraps the C
+restatement in oracle.c, which cites the reference file:line it follows.
+
+Build with `make -C oracle` (also done by __graft_entry__.build()).
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+
+RRO_OK = 0
+RRO_EINVAL = -1
+RRO_EOVERFLOW = -2
+PERM_FAILURES = {
+    1: "id_range",
+    2: "position_range",
+    4: "expert_segment",
+    8: "bijection",
+    16: "inverse_mapping",
+    32: "row_copy",
+    64: "offsets",
+}
+
+
+class OracleError(ValueError):
+    """The reference oracle would throw (invalid shape, id out of range, overflow)."""
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    return LIB_PATH
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp = c_void_p
+    sig = {
+        "rro_dense_gemm_f64": (c_int, [vp, vp, vp, c_int, c_int, c_int]),
+        "rro_dense_gemm_f32_seq": (None, [vp, vp, vp, c_int, c_int, c_int]),
+        "rro_top2_f32": (c_int, [vp, c_int, c_int, vp, vp]),
+        "rro_top2_f64": (c_int, [vp, c_int, c_int, vp, vp]),
+        "rro_histogram": (c_int, [vp, c_int64, c_int, vp]),
+        "rro_exclusive_scan": (c_int, [vp, c_int, vp]),
+        "rro_stable_route_pos": (c_int, [vp, c_int64, vp, c_int, vp]),
+        "rro_inverse_route": (c_int, [vp, c_int64, vp]),
+        "rro_permute_rows": (None, [vp, vp, c_int, c_int, c_int, vp]),
+        "rro_validate_permute": (c_int, [vp, vp, vp, c_int, vp, vp, vp, c_int, c_int, c_int]),
+        "rro_grouped_gemm_f64": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_grouped_gemm_f32_seq": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_unpermute_f64": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_unpermute_f32": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_chain_output_f32": (None, [vp, vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_chain": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int, c_int, c_int, vp, vp, vp, vp, vp, vp]),
+        "rro_compare_floating": (c_int64, [vp, vp, c_int64, c_double, c_double, POINTER(c_double), POINTER(c_double)]),
+        "rro_compare_gemm": (c_int64, [vp, vp, vp, vp, c_int, c_int, c_int, POINTER(c_double), POINTER(c_double)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = _load()
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+def _check(rc: int) -> None:
+    if rc == RRO_EINVAL:
+        raise OracleError("invalid shape or route id out of range")
+    if rc == RRO_EOVERFLOW:
+        raise OracleError("int32 overflow")
+
+
+def dense_gemm_f64(a, b):
+    """reference src/dense_gemm/cpu_reference/reference.cpp:10-35"""
+    a = _c(a, np.float64); b = _c(b, np.float64)
+    m, k = a.shape; k2, n = b.shape
+    assert k == k2
+    c = np.empty((m, n), np.float64)
+    _check(_lib.rro_dense_gemm_f64(_p(a), _p(b), _p(c), m, n, k))
+    return c
+
+
+def dense_gemm_f32_seq(a, b):
+    """reference benchmarks/adapters/chain_adapter.cpp:197-206"""
+    a = _c(a, np.float32); b = _c(b, np.float32)
+    m, k = a.shape; _, n = b.shape
+    c = np.empty((m, n), np.float32)
+    _lib.rro_dense_gemm_f32_seq(_p(a), _p(b), _p(c), m, n, k)
+    return c
+
+
+def top2_f32(logits):
+    """reference include/raggedroute/benchmark/adapter_utils.h:363-418"""
+    logits = _c(logits, np.float32)
+    t, e = logits.shape
+    ids = np.empty((t, 2), np.int32); w = np.empty((t, 2), np.float32)
+    _check(_lib.rro_top2_f32(_p(logits), t, e, _p(ids), _p(w)))
+    return ids, w
+
+
+def top2_f64(logits):
+    """reference src/topk_gate/cpu_reference/reference.cpp:12-72"""
+    logits = _c(logits, np.float64)
+    t, e = logits.shape
+    ids = np.empty((t, 2), np.int32); w = np.empty((t, 2), np.float64)
+    _check(_lib.rro_top2_f64(_p(logits), t, e, _p(ids), _p(w)))
+    return ids, w
+
+
+def histogram(ids, experts):
+    """reference src/histogram/cpu_reference/reference.cpp:11-22"""
+    ids = _c(ids, np.int32).reshape(-1)
+    counts = np.empty(experts, np.int32)
+    _check(_lib.rro_histogram(_p(ids), ids.size, experts, _p(counts)))
+    return counts
+
+
+def exclusive_scan(counts):
+    """reference src/scan/cpu_reference/reference.cpp:9-20"""
+    counts = _c(counts, np.int32).reshape(-1)
+    offsets = np.empty(counts.size + 1, np.int32)
+    _check(_lib.rro_exclusive_scan(_p(counts), counts.size, _p(offsets)))
+    return offsets
+
+
+def stable_route_pos(ids, offsets):
+    """reference benchmarks/adapters/unpermute_adapter.cpp:47-53"""
+    ids = _c(ids, np.int32).reshape(-1); offsets = _c(offsets, np.int32)
+    pos = np.empty(ids.size, np.int32)
+    _check(_lib.rro_stable_route_pos(_p(ids), ids.size, _p(offsets), offsets.size - 1, _p(pos)))
+    return pos
+
+
+def inverse_route(route_pos):
+    route_pos = _c(route_pos, np.int32).reshape(-1)
+    out = np.empty(route_pos.size, np.int32)
+    _check(_lib.rro_inverse_route(_p(route_pos), route_pos.size, _p(out)))
+    return out
+
+
+def permute_rows(x, route_pos, top_k):
+    x = _c(x, np.float32); route_pos = _c(route_pos, np.int32).reshape(-1)
+    t, h = x.shape
+    out = np.empty((t * top_k, h), np.float32)
+    _lib.rro_permute_rows(_p(x), _p(route_pos), t, top_k, h, _p(out))
+    return out
+
+
+def validate_permute(x, ids, offsets, x_permuted, route_pos, sorted_route, top_k):
+    """reference src/permute/cpu_reference/reference.cpp:22-81; returns failed invariant names."""
+    x = _c(x, np.float32); ids = _c(ids, np.int32).reshape(-1); offsets = _c(offsets, np.int32)
+    xp = _c(x_permuted, np.float32); rp = _c(route_pos, np.int32).reshape(-1)
+    sr = None if sorted_route is None else _c(sorted_route, np.int32).reshape(-1)
+    t, h = x.shape
+    bits = _lib.rro_validate_permute(_p(x), _p(ids), _p(offsets), offsets.size - 1, _p(xp), _p(rp),
+                                     _p(sr), t, top_k, h)
+    return [name for bit, name in PERM_FAILURES.items() if bits & bit]
+
+
+def grouped_gemm_f64(x, w, offsets):
+    """reference src/grouped_gemm/cpu_reference/reference.cpp:10-44"""
+    x = _c(x, np.float64); w = _c(w, np.float64); offsets = _c(offsets, np.int32)
+    e, h, o = w.shape
+    y = np.empty((int(offsets[-1]), o), np.float64)
+    _check(_lib.rro_grouped_gemm_f64(_p(x), _p(w), _p(offsets), e, h, o, _p(y)))
+    return y
+
+
+def grouped_gemm_f32_seq(x, w, offsets):
+    x = _c(x, np.float32); w = _c(w, np.float32); offsets = _c(offsets, np.int32)
+    e, h, o = w.shape
+    y = np.empty((int(offsets[-1]), o), np.float32)
+    _check(_lib.rro_grouped_gemm_f32_seq(_p(x), _p(w), _p(offsets), e, h, o, _p(y)))
+    return y
+
+
+def unpermute_f64(y_permuted, route_pos, route_weights, top_k):
+    """reference src/unpermute/cpu_reference/reference.cpp:10-36"""
+    yp = _c(y_permuted, np.float64); rp = _c(route_pos, np.int32).reshape(-1)
+    w = _c(route_weights, np.float64).reshape(-1)
+    t = rp.size // top_k; o = yp.shape[1]
+    y = np.empty((t, o), np.float64)
+    _check(_lib.rro_unpermute_f64(_p(yp), _p(rp), _p(w), t, top_k, o, _p(y)))
+    return y
+
+
+def unpermute_f32(y_permuted, route_pos, route_weights, top_k):
+    """reference benchmarks/adapters/unpermute_adapter.cpp:63-73"""
+    yp = _c(y_permuted, np.float32); rp = _c(route_pos, np.int32).reshape(-1)
+    w = _c(route_weights, np.float32).reshape(-1)
+    t = rp.size // top_k; o = yp.shape[1]
+    y = np.empty((t, o), np.float32)
+    _check(_lib.rro_unpermute_f32(_p(yp), _p(rp), _p(w), t, top_k, o, _p(y)))
+    return y
+
+
+def chain_output_f32(x, expert_weights, ids, route_weights):
+    """reference benchmarks/adapters/chain_adapter.cpp:858-879"""
+    x = _c(x, np.float32); we = _c(expert_weights, np.float32)
+    ids = _c(ids, np.int32); rw = _c(route_weights, np.float32)
+    t, h = x.shape; o = we.shape[2]
+    y = np.empty((t, o), np.float32)
+    _lib.rro_chain_output_f32(_p(x), _p(we), _p(ids), _p(rw), t, h, o, _p(y))
+    return y
+
+
+def chain(x, expert_weights, *, router_weights=None, logits=None):
+    """Full reference chain oracle (reference chain_adapter.cpp:188-239).
+
+    chain_from_tokens when router_weights is given, chain_from_logits when
+    logits is given. Returns a dict of every intermediate.
+    """
+    x = _c(x, np.float32); we = _c(expert_weights, np.float32)
+    t, h = x.shape; e, _, o = we.shape
+    from_tokens = router_weights is not None
+    if from_tokens:
+        rw = _c(router_weights, np.float32)
+        lg = np.empty((t, e), np.float32)
+    else:
+        rw = None
+        lg = _c(logits, np.float32).copy()
+    out = {
+        "ids": np.empty((t, 2), np.int32), "weights": np.empty((t, 2), np.float32),
+        "counts": np.empty(e, np.int32), "offsets": np.empty(e + 1, np.int32),
+        "route_pos": np.empty(t * 2, np.int32), "y": np.empty((t, o), np.float32),
+    }
+    _check(_lib.rro_chain(_p(x), _p(rw), _p(lg), int(from_tokens), _p(we), t, e, h, o,
+                          _p(out["ids"]), _p(out["weights"]), _p(out["counts"]),
+                          _p(out["offsets"]), _p(out["route_pos"]), _p(out["y"])))
+    out["logits"] = lg
+    return out
+
+
+def compare_floating(actual, expected, atol, rtol):
+    """reference src/correctness/reference_validation.cpp:32-68 -> (failures, max_abs, max_rel)"""
+    a = _c(actual, np.float64).reshape(-1); e = _c(expected, np.float64).reshape(-1)
+    assert a.size == e.size
+    ma, mr = c_double(0.0), c_double(0.0)
+    fails = _lib.rro_compare_floating(_p(a), _p(e), a.size, atol, rtol, ctypes.byref(ma), ctypes.byref(mr))
+    return int(fails), ma.value, mr.value
+
+
+def compare_gemm(actual, expected, a, b):
+    """reference src/correctness/reference_validation.cpp:70-115 -> (failures, max_abs, worst ratio)"""
+    act = _c(actual, np.float64); exp = _c(expected, np.float64)
+    a = _c(a, np.float64); b = _c(b, np.float64)
+    m, k = a.shape; _, n = b.shape
+    ma, wr = c_double(0.0), c_double(0.0)
+    fails = _lib.rro_compare_gemm(_p(act), _p(exp), _p(a), _p(b), m, n, k, ctypes.byref(ma), ctypes.byref(wr))
+    return int(fails), ma.value, wr.value

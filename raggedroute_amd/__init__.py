@@ -1,0 +1,239 @@
+"""RaggedRoute routing pipeline for AMD MI355X (gfx950).
+
+Python mirror of the C++ v0.2 operator API (reference
+include/raggedroute/operators.h:114-135, dispatch.h:32-46, baseline_ops.h:14-42)
+over the C ABI of libraggedroute_amd.so. All compute runs in the HIP library;
+this module only marshals arguments. Importing it loads the library and fails
+loudly when it is missing or incomplete: there is no fallback path.
+
+Device memory comes from the caller (for example torch tensors on a ROCm
+device); pass raw device pointers (``tensor.data_ptr()``) and the HIP stream
+handle (``torch.cuda.current_stream().cuda_stream``).
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import byref
+from pathlib import Path
+
+from ._capi import (  # noqa: F401  (re-exported vocabulary)
+    GFX950_NATIVE,
+    MAX_EXPERTS,
+    PROTOTYPES,
+    ChainArgs,
+    ConstTensorView,
+    DenseGemmArgs,
+    DeviceArchitecture,
+    DispatchDecision,
+    DispatchRequest,
+    ExclusiveScanArgs,
+    GroupedGemmArgs,
+    HistogramArgs,
+    HistogramExclusiveScanArgs,
+    KernelFamily,
+    KernelSelection,
+    MutableTensorView,
+    OperatorKind,
+    OperatorSignature,
+    RuntimeContext,
+    ScalarType,
+    Status,
+    StatusCode,
+    TensorLayout,
+    TensorSpec,
+    TokenPermuteArgs,
+    TopKGateArgs,
+    UnpermuteArgs,
+    bind,
+)
+
+LIB_PATH = Path(__file__).resolve().parent / "libraggedroute_amd.so"
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m raggedroute_amd.build` "
+            "(there is no non-HIP fallback)"
+        )
+    return bind(ctypes.CDLL(str(LIB_PATH)))
+
+
+lib = _load()
+
+
+def _ctx(context: RuntimeContext | None) -> RuntimeContext:
+    return context if context is not None else RuntimeContext()
+
+
+# ---- operator wrappers (reference include/raggedroute/operators.h:127-135) ----
+
+def dense_gemm(args: DenseGemmArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_dense_gemm(byref(args), byref(_ctx(context)))
+
+
+def topk_gate(args: TopKGateArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_topk_gate(byref(args), byref(_ctx(context)))
+
+
+def histogram(args: HistogramArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_histogram(byref(args), byref(_ctx(context)))
+
+
+def exclusive_scan(args: ExclusiveScanArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_exclusive_scan(byref(args), byref(_ctx(context)))
+
+
+def histogram_exclusive_scan(args: HistogramExclusiveScanArgs,
+                             context: RuntimeContext | None = None) -> Status:
+    return lib.rr_histogram_exclusive_scan(byref(args), byref(_ctx(context)))
+
+
+def token_permute(args: TokenPermuteArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_token_permute(byref(args), byref(_ctx(context)))
+
+
+def grouped_gemm(args: GroupedGemmArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_grouped_gemm(byref(args), byref(_ctx(context)))
+
+
+def unpermute(args: UnpermuteArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_unpermute(byref(args), byref(_ctx(context)))
+
+
+def chain_from_tokens(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_chain_from_tokens(byref(args), byref(_ctx(context)))
+
+
+def chain_from_logits(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_chain_from_logits(byref(args), byref(_ctx(context)))
+
+
+# ---- workspace queries (reference operators.h:114-122) ----
+
+def get_dense_gemm_workspace_size(args: DenseGemmArgs) -> int:
+    return lib.rr_dense_gemm_workspace_size(byref(args))
+
+
+def get_topk_gate_workspace_size(args: TopKGateArgs) -> int:
+    return lib.rr_topk_gate_workspace_size(byref(args))
+
+
+def get_histogram_workspace_size(args: HistogramArgs) -> int:
+    return lib.rr_histogram_workspace_size(byref(args))
+
+
+def get_exclusive_scan_workspace_size(args: ExclusiveScanArgs) -> int:
+    return lib.rr_exclusive_scan_workspace_size(byref(args))
+
+
+def get_histogram_exclusive_scan_workspace_size(args: HistogramExclusiveScanArgs) -> int:
+    return lib.rr_histogram_exclusive_scan_workspace_size(byref(args))
+
+
+def get_token_permute_workspace_size(args: TokenPermuteArgs) -> int:
+    return lib.rr_token_permute_workspace_size(byref(args))
+
+
+def get_grouped_gemm_workspace_size(args: GroupedGemmArgs) -> int:
+    return lib.rr_grouped_gemm_workspace_size(byref(args))
+
+
+def get_unpermute_workspace_size(args: UnpermuteArgs) -> int:
+    return lib.rr_unpermute_workspace_size(byref(args))
+
+
+def get_chain_workspace_size(args: ChainArgs) -> int:
+    return lib.rr_chain_workspace_size(byref(args))
+
+
+# ---- dispatch (reference include/raggedroute/dispatch.h:32-46) ----
+
+def classify_compute_capability(major: int, minor: int) -> DeviceArchitecture:
+    return DeviceArchitecture(lib.rr_classify_compute_capability(major, minor))
+
+
+def classify_gcn_arch_name(name: str) -> DeviceArchitecture:
+    return DeviceArchitecture(lib.rr_classify_gcn_arch_name(name.encode()))
+
+
+def query_current_device_architecture() -> tuple[Status, DeviceArchitecture]:
+    out = ctypes.c_int32(0)
+    status = lib.rr_query_current_device_architecture(byref(out))
+    return status, DeviceArchitecture(out.value) if status.ok() else DeviceArchitecture.kOther
+
+
+def resolve_device_architecture(requested: DeviceArchitecture) -> tuple[Status, DeviceArchitecture]:
+    out = ctypes.c_int32(0)
+    status = lib.rr_resolve_device_architecture(int(requested), byref(out))
+    return status, DeviceArchitecture(out.value) if status.ok() else DeviceArchitecture.kOther
+
+
+def select_kernel(request: DispatchRequest, decision: DispatchDecision | None) -> Status:
+    return lib.rr_select_kernel(byref(request), byref(decision) if decision is not None else None)
+
+
+# ---- low-level launchers (reference include/raggedroute/baseline_ops.h:14-42) ----
+
+class ops:  # noqa: N801  (mirrors the reference namespace raggedroute::ops)
+    """Naive HIP baselines: reference semantics, no resets, hipError_t results."""
+
+    @staticmethod
+    def launch_dense_gemm_naive(a, b, c, m, n, k, stream=None) -> int:
+        return lib.rr_launch_dense_gemm_naive(a, b, c, m, n, k, stream)
+
+    @staticmethod
+    def launch_topk_gate_naive(logits, expert_ids, weights, tokens, experts, stream=None) -> int:
+        return lib.rr_launch_topk_gate_naive(logits, expert_ids, weights, tokens, experts, stream)
+
+    @staticmethod
+    def launch_histogram_naive(expert_ids, counts, route_pairs, experts, stream=None) -> int:
+        return lib.rr_launch_histogram_naive(expert_ids, counts, route_pairs, experts, stream)
+
+    @staticmethod
+    def launch_exclusive_scan_naive(counts, offsets, experts, stream=None) -> int:
+        return lib.rr_launch_exclusive_scan_naive(counts, offsets, experts, stream)
+
+    @staticmethod
+    def launch_token_permute_naive(x, expert_ids, offsets, cursors, x_permuted, route_pos,
+                                   sorted_route, tokens, top_k, hidden, stream=None) -> int:
+        return lib.rr_launch_token_permute_naive(x, expert_ids, offsets, cursors, x_permuted,
+                                                 route_pos, sorted_route, tokens, top_k, hidden,
+                                                 stream)
+
+    @staticmethod
+    def launch_grouped_gemm_naive(x_permuted, expert_weights, offsets, y_permuted, experts,
+                                  hidden, output, max_expert_tokens, stream=None) -> int:
+        return lib.rr_launch_grouped_gemm_naive(x_permuted, expert_weights, offsets, y_permuted,
+                                                experts, hidden, output, max_expert_tokens, stream)
+
+    @staticmethod
+    def launch_unpermute_naive(y_permuted, route_pos, route_weights, y, tokens, top_k, output,
+                               stream=None) -> int:
+        return lib.rr_launch_unpermute_naive(y_permuted, route_pos, route_weights, y, tokens,
+                                             top_k, output, stream)
+
+    @staticmethod
+    def launch_cache_scrub(buffer, elements, stream=None) -> int:
+        return lib.rr_launch_cache_scrub(buffer, elements, stream)
+
+
+def fill_uniform(ptr, count, seed, stream_id, low, high, stream=None) -> int:
+    return lib.rr_fill_uniform(ptr, count, seed, stream_id, low, high, stream)
+
+
+def fill_normal(ptr, count, seed, stream_id, mean, stddev, stream=None) -> int:
+    return lib.rr_fill_normal(ptr, count, seed, stream_id, mean, stddev, stream)
+
+
+def kernel(family: KernelFamily = KernelFamily.kAuto, implementation_id: int = 0) -> KernelSelection:
+    return KernelSelection(int(family), implementation_id)
+
+
+def cview(ptr) -> ConstTensorView:
+    """FP32 row-major view of a device pointer (int or None)."""
+    return ConstTensorView(ptr, TensorSpec())
+
+
+def mview(ptr) -> MutableTensorView:
+    return MutableTensorView(ptr, TensorSpec())

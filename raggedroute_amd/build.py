@@ -1,0 +1,89 @@
+"""Build recipe for libraggedroute_amd.so (gfx950).
+
+HIP sources (*.hip) are compiled with hipcc for gfx950 only; host-only C++
+sources (*.cpp) with g++ against the HIP headers. Objects go to _build/ at the
+repository root and the shared library is written in-tree next to this file so
+that it travels with the repository snapshot.
+
+    python -m raggedroute_amd.build          # full rebuild
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = REPO / "include"
+BUILD = REPO / "_build"
+LIB_NAME = "libraggedroute_amd.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    # Packed FP32 instructions stay disabled: scalar/float2 code only.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__"]
+
+
+def _hipcc() -> str:
+    path = ROCM / "bin" / "hipcc"
+    if not path.exists():
+        raise RuntimeError(f"hipcc not found at {path}")
+    return str(path)
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            "command failed (%d): %s\n%s%s" % (proc.returncode, " ".join(cmd), proc.stdout, proc.stderr)
+        )
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.name + ".o")
+    includes = [f"-I{INCLUDE}", f"-I{CSRC}"]
+    if src.suffix == ".hip":
+        cmd = [_hipcc(), *HIP_FLAGS, *includes, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = ["g++", *CXX_FLAGS, *includes, f"-I{ROCM / 'include'}", "-c", str(src), "-o", str(obj)]
+    _run(cmd)
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every source and link the shared library; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+    if not sources:
+        raise RuntimeError(f"no sources under {CSRC}")
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([_hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp),
+          *map(str, objects), f"-L{ROCM / 'lib'}", "-lamdhip64",
+          f"-Wl,-rpath,{ROCM / 'lib'}"])
+    shutil.move(str(tmp), str(LIB_PATH))
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,159 @@
+// Chain entries: chain_from_tokens (7 stages) and chain_from_logits (6 stages).
+//
+// The stage order is the one of reference benchmarks/adapters/chain_adapter.cpp:263-467:
+// dense GEMM -> top-2 gate -> histogram+scan -> token permute -> grouped GEMM
+// -> unpermute, all on the caller's stream, with no host synchronisation; the
+// grouped GEMM gets the worst-case launch bound max_expert_tokens = R
+// (reference chain_adapter.cpp:391-401). Each stage goes through the public C
+// ABI entry, so stage validation is identical to calling the operators one by one.
+#include <climits>
+#include <cstddef>
+#include <cstdint>
+
+#include "common.h"
+
+namespace rr {
+namespace {
+
+rr_const_tensor_view cview(const void* data) noexcept { return {data, default_spec()}; }
+rr_mutable_tensor_view mview(void* data) noexcept { return {data, default_spec()}; }
+
+rr_status validate_chain(const rr_chain_args* a, const rr_runtime_context* context,
+                         bool from_tokens) noexcept {
+  if (a == nullptr) return invalid_argument("chain args must not be null");
+  if (context == nullptr) return invalid_argument("runtime context must not be null");
+  if (a->tokens < 0 || a->experts < 2 || a->experts > RR_MAX_EXPERTS || a->top_k != 2 ||
+      a->hidden < 0 || a->output < 0) {
+    return invalid_argument("chain requires T>=0, 2<=E<=1024, top_k=2, K>=0 and N>=0");
+  }
+  if (a->tokens > INT_MAX / 2) return invalid_argument("chain route count exceeds int32 indexing");
+  if (a->tokens > 0 && a->output > 0 && a->tokens > INT_MAX / a->output) {
+    return invalid_argument("chain output count exceeds int32 indexing");
+  }
+  if (a->tokens == 0) return ok_status();
+  if (a->logits == nullptr || a->expert_ids == nullptr || a->route_weights == nullptr ||
+      a->counts == nullptr || a->offsets == nullptr || a->route_pos == nullptr ||
+      a->y_permuted == nullptr || a->y == nullptr) {
+    return invalid_argument("chain received a null device pointer");
+  }
+  if (a->hidden != 0 && (a->x == nullptr || a->x_permuted == nullptr ||
+                         a->expert_weights == nullptr ||
+                         (from_tokens && a->router_weights == nullptr))) {
+    return invalid_argument("chain received a null device pointer");
+  }
+  const size_t cursor_bytes = static_cast<size_t>(a->experts) * sizeof(int32_t);
+  if (context->workspace == nullptr || context->workspace_bytes < cursor_bytes) {
+    return make_status(RR_STATUS_INSUFFICIENT_WORKSPACE,
+                       "chain requires int32 cursor workspace for every expert");
+  }
+  return ok_status();
+}
+
+rr_status run_chain(const rr_chain_args* a, const rr_runtime_context* context,
+                    bool from_tokens) noexcept {
+  rr_status status = validate_chain(a, context, from_tokens);
+  if (status.code != RR_STATUS_SUCCESS || a->tokens == 0) return status;
+
+  rr_runtime_context ctx = *context;
+  status = rr_resolve_device_architecture(context->architecture, &ctx.architecture);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+  const int32_t routes = a->tokens * 2;
+  // An optimized request selects the native kernel of every stage (operator-local
+  // ids do not carry across stages); auto and naive pass through unchanged.
+  rr_kernel_selection kernel = a->kernel;
+  if (kernel.family == RR_FAMILY_OPTIMIZED) kernel.implementation_id = RR_IMPL_GFX950_NATIVE;
+
+  if (from_tokens) {
+    rr_dense_gemm_args dense{};
+    dense.a = cview(a->x);
+    dense.b = cview(a->router_weights);
+    dense.c = mview(a->logits);
+    dense.m = a->tokens;
+    dense.n = a->experts;
+    dense.k = a->hidden;
+    dense.alpha = 1.0F;
+    dense.beta = 0.0F;
+    dense.accumulator_dtype = RR_DTYPE_FP32;
+    dense.kernel = kernel;
+    status = rr_dense_gemm(&dense, &ctx);
+    if (status.code != RR_STATUS_SUCCESS) return status;
+  }
+
+  rr_topk_gate_args gate{};
+  gate.logits = cview(a->logits);
+  gate.expert_ids = a->expert_ids;
+  gate.weights = mview(a->route_weights);
+  gate.tokens = a->tokens;
+  gate.experts = a->experts;
+  gate.top_k = 2;
+  gate.accumulator_dtype = RR_DTYPE_FP32;
+  gate.kernel = kernel;
+  status = rr_topk_gate(&gate, &ctx);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+
+  rr_histogram_exclusive_scan_args meta{};
+  meta.expert_ids = a->expert_ids;
+  meta.counts = a->counts;
+  meta.offsets = a->offsets;
+  meta.route_pairs = routes;
+  meta.experts = a->experts;
+  meta.kernel = kernel;
+  status = rr_histogram_exclusive_scan(&meta, &ctx);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+
+  rr_token_permute_args permute{};
+  permute.x = cview(a->x);
+  permute.expert_ids = a->expert_ids;
+  permute.offsets = a->offsets;
+  permute.x_permuted = mview(a->x_permuted);
+  permute.route_pos = a->route_pos;
+  permute.sorted_route = a->sorted_route;
+  permute.tokens = a->tokens;
+  permute.experts = a->experts;
+  permute.top_k = 2;
+  permute.hidden = a->hidden;
+  permute.kernel = kernel;
+  status = rr_token_permute(&permute, &ctx);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+
+  rr_grouped_gemm_args grouped{};
+  grouped.x_permuted = cview(a->x_permuted);
+  grouped.expert_weights = cview(a->expert_weights);
+  grouped.offsets = a->offsets;
+  grouped.y_permuted = mview(a->y_permuted);
+  grouped.experts = a->experts;
+  grouped.hidden = a->hidden;
+  grouped.output = a->output;
+  grouped.max_expert_tokens = routes;
+  grouped.accumulator_dtype = RR_DTYPE_FP32;
+  grouped.kernel = kernel;
+  status = rr_grouped_gemm(&grouped, &ctx);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+
+  rr_unpermute_args unpermute{};
+  unpermute.y_permuted = cview(a->y_permuted);
+  unpermute.route_pos = a->route_pos;
+  unpermute.route_weights = cview(a->route_weights);
+  unpermute.y = mview(a->y);
+  unpermute.tokens = a->tokens;
+  unpermute.top_k = 2;
+  unpermute.output = a->output;
+  unpermute.accumulator_dtype = RR_DTYPE_FP32;
+  unpermute.kernel = kernel;
+  return rr_unpermute(&unpermute, &ctx);
+}
+
+}  // namespace
+}  // namespace rr
+
+extern "C" {
+
+rr_status rr_chain_from_tokens(const rr_chain_args* args, const rr_runtime_context* context) {
+  return rr::run_chain(args, context, true);
+}
+
+rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_context* context) {
+  return rr::run_chain(args, context, false);
+}
+
+}  // extern "C"

@@ -1,0 +1,361 @@
+// FP32 GEMMs on gfx950 matrix cores (v_mfma_f32_16x16x4_f32).
+//
+// One persistent kernel serves both the router dense GEMM (one segment of M
+// rows) and the ragged grouped GEMM (segments [offsets[e], offsets[e+1]) with
+// weights W[e]). The host never reads offsets: every workgroup loads them to
+// LDS, builds the per-expert row-tile prefix and walks the tile space
+// (row tiles of every expert x column tiles) with a grid-stride loop.
+//
+// Tile: BM x BN per workgroup, BK = 16 per LDS stage, two LDS stages plus a
+// register prefetch of the next stage. LDS holds both operands k-contiguous
+// ([m][k] and [n][k], rows padded to 20 floats) so every MFMA operand fetch is
+// one ds_read_b128 covering four consecutive MFMA k-steps. Lane l (group
+// g = l / 16, index i = l % 16) supplies A[m0 + i][k] and B[k][n0 + i] for
+// k = kk + 4g + s at MFMA step s, which is the same k for both operands.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+#include <cstddef>
+#include <cstdint>
+
+#include "launchers.h"
+#include "raggedroute_capi.h"
+#include "wave.h"
+
+namespace rr::kern {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kBK = 16;
+constexpr int kLd = kBK + 4;  // padded LDS row (floats)
+constexpr int kGroupM = 8;    // row tiles per swizzle group
+constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dispatched round-robin
+
+template <int BM_, int BN_, int WM_, int WN_>
+struct TileShape {
+  static constexpr int BM = BM_;
+  static constexpr int BN = BN_;
+  static constexpr int WM = WM_;
+  static constexpr int WN = WN_;
+  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int kTM = BM / WM / 16;  // 16x16 MFMA tiles per wave along M
+  static constexpr int kTN = BN / WN / 16;
+  static constexpr int kALoads = BM * kBK / 4 / kThreads;  // float4 slots per thread
+  static constexpr int kBLoads = BN * kBK / 4 / kThreads;
+  static constexpr int kStageFloats = (BM + BN) * kLd;
+  static_assert(kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
+  static_assert(BM * kBK / 4 % kThreads == 0 && BN * kBK / 4 % kThreads == 0, "uneven loads");
+};
+
+// Global -> register staging of one BK slice. A rows are k-contiguous in
+// global memory; B rows are n-contiguous and are transposed on the LDS store.
+template <class S, bool VEC>
+struct Stage {
+  float a[S::kALoads][4];
+  float b[S::kBLoads][4];
+
+  __device__ __forceinline__ void load(const float* __restrict__ A, const float* __restrict__ B,
+                                       int row0, int row_end, int n0, int N, int K, int k0,
+                                       int tid) {
+#pragma unroll
+    for (int p = 0; p < S::kALoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int r = f >> 2;            // BK / 4 = 4 float4 per row
+      const int c = (f & 3) * 4;
+      const int row = row0 + r;
+      const int k = k0 + c;
+      const float* src = A + static_cast<std::size_t>(row) * K + k;
+      if (VEC) {
+        if (row < row_end && k < K) {
+          const float4 v = *reinterpret_cast<const float4*>(src);
+          a[p][0] = v.x; a[p][1] = v.y; a[p][2] = v.z; a[p][3] = v.w;
+        } else {
+          a[p][0] = a[p][1] = a[p][2] = a[p][3] = 0.0F;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[p][j] = (row < row_end && k + j < K) ? src[j] : 0.0F;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < S::kBLoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int kr = f & (kBK - 1);  // k varies fastest across lanes
+      const int n = (f >> 4) * 4;
+      const int k = k0 + kr;
+      const int col = n0 + n;
+      const float* src = B + static_cast<std::size_t>(k) * N + col;
+      if (VEC) {
+        if (k < K && col < N) {
+          const float4 v = *reinterpret_cast<const float4*>(src);
+          b[p][0] = v.x; b[p][1] = v.y; b[p][2] = v.z; b[p][3] = v.w;
+        } else {
+          b[p][0] = b[p][1] = b[p][2] = b[p][3] = 0.0F;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[p][j] = (k < K && col + j < N) ? src[j] : 0.0F;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ lds, int tid) const {
+    float* As = lds;
+    float* Bs = lds + S::BM * kLd;
+#pragma unroll
+    for (int p = 0; p < S::kALoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int r = f >> 2;
+      const int c = (f & 3) * 4;
+      *reinterpret_cast<float4*>(As + r * kLd + c) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
+    }
+#pragma unroll
+    for (int p = 0; p < S::kBLoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int kr = f & (kBK - 1);
+      const int n = (f >> 4) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Bs[(n + j) * kLd + kr] = b[p][j];
+    }
+  }
+};
+
+// Tile space decode: row tiles are grouped kGroupM at a time so that workgroups
+// running together share both A row blocks and B column strips.
+__device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles, int* rt, int* ct) {
+  const int group_size = kGroupM * col_tiles;
+  const int group = t / group_size;
+  const int first = group * kGroupM;
+  const int rows_in_group = row_tiles - first < kGroupM ? row_tiles - first : kGroupM;
+  const int within = t - group * group_size;
+  *rt = first + within % rows_in_group;
+  *ct = within / rows_in_group;
+}
+
+template <class S, bool VEC>
+__global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
+    const float* __restrict__ X, const float* __restrict__ W, const int32_t* __restrict__ offsets,
+    float* __restrict__ Y, int experts, int dense_rows, int K, int N) {
+  extern __shared__ float lds[];
+  float* stages = lds;                                              // 2 stages
+  int32_t* s_off = reinterpret_cast<int32_t*>(lds + 2 * S::kStageFloats);  // [experts + 1]
+  int32_t* s_pre = s_off + experts + 1;                             // [experts + 1]
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = rr::dev::lane_id();
+  const int wave = tid >> 6;
+
+  // ---- device-side scheduler: per-expert row-tile prefix in LDS ----
+  for (int e = tid; e <= experts; e += S::kThreads) {
+    s_off[e] = offsets != nullptr ? offsets[e] : (e == 0 ? 0 : dense_rows);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // Lane l owns experts [l*per, (l+1)*per); experts <= 1024 -> per <= 16.
+    const int per = (experts + 63) / 64;
+    int32_t local = 0;
+    for (int j = 0; j < per; ++j) {
+      const int e = lane * per + j;
+      if (e < experts) {
+        const int32_t cnt = s_off[e + 1] - s_off[e];
+        local += cnt > 0 ? (cnt + S::BM - 1) / S::BM : 0;
+      }
+    }
+    const int32_t incl = rr::dev::wave_inclusive_scan(local);
+    int32_t run = incl - local;
+    for (int j = 0; j < per; ++j) {
+      const int e = lane * per + j;
+      if (e < experts) {
+        s_pre[e] = run;
+        const int32_t cnt = s_off[e + 1] - s_off[e];
+        run += cnt > 0 ? (cnt + S::BM - 1) / S::BM : 0;
+      }
+    }
+    if (lane == 63) s_pre[experts] = incl;
+  }
+  __syncthreads();
+  const int row_tiles = s_pre[experts];
+  const int col_tiles = (N + S::BN - 1) / S::BN;
+  const long total = static_cast<long>(row_tiles) * col_tiles;
+
+  // Workgroups are dispatched round-robin over the XCDs; give the workgroups
+  // of one XCD consecutive tile ids so their operands meet in the same L2.
+  const int grid = static_cast<int>(gridDim.x);
+  const int b = static_cast<int>(blockIdx.x);
+  const int worker = (grid % kXcds == 0) ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
+
+  const int wm0 = (wave / S::WN) * (S::BM / S::WM);
+  const int wn0 = (wave % S::WN) * (S::BN / S::WN);
+  const int g = lane >> 4;
+  const int li = lane & 15;
+  const int nk = (K + kBK - 1) / kBK;
+
+  for (long t = worker; t < total; t += grid) {
+    int rt, ct;
+    decode_tile(static_cast<int>(t), row_tiles, col_tiles, &rt, &ct);
+    // expert = last e with s_pre[e] <= rt (binary search over the prefix)
+    int lo = 0, hi = experts - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pre[mid] <= rt) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int row0 = s_off[e] + (rt - s_pre[e]) * S::BM;
+    const int row_end = s_off[e + 1];
+    const int n0 = ct * S::BN;
+    const float* B = W + static_cast<std::size_t>(offsets != nullptr ? e : 0) * K * N;
+
+    v4f acc[S::kTM][S::kTN];
+#pragma unroll
+    for (int i = 0; i < S::kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::kTN; ++j) acc[i][j] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+
+    Stage<S, VEC> st;
+    if (nk > 0) {
+      st.load(X, B, row0, row_end, n0, N, K, 0, tid);
+      st.store(stages, tid);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const float* cur = stages + (kt & 1) * S::kStageFloats;
+      if (kt + 1 < nk) st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * kBK, tid);
+      const float* As = cur;
+      const float* Bs = cur + S::BM * kLd;
+#pragma unroll
+      for (int kk = 0; kk < kBK; kk += 16) {
+        float4 af[S::kTM], bf[S::kTN];
+#pragma unroll
+        for (int i = 0; i < S::kTM; ++i) {
+          af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * kLd + kk + 4 * g);
+        }
+#pragma unroll
+        for (int j = 0; j < S::kTN; ++j) {
+          bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * kLd + kk + 4 * g);
+        }
+#pragma unroll
+        for (int i = 0; i < S::kTM; ++i) {
+#pragma unroll
+          for (int j = 0; j < S::kTN; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+      if (kt + 1 < nk) st.store(stages + ((kt + 1) & 1) * S::kStageFloats, tid);
+      __syncthreads();
+    }
+
+    // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
+#pragma unroll
+    for (int i = 0; i < S::kTM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + wm0 + i * 16 + 4 * g + r;
+        if (row >= row_end) continue;
+        float* yrow = Y + static_cast<std::size_t>(row) * N;
+#pragma unroll
+        for (int j = 0; j < S::kTN; ++j) {
+          const int col = n0 + wn0 + j * 16 + li;
+          if (col < N) yrow[col] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices] = {};
+
+int device_cu_count() {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 256;
+  if (device >= 0 && device < kMaxDevices) {
+    const int cached = g_cu_count[device].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0) {
+    cus = 256;
+  }
+  if (device >= 0 && device < kMaxDevices) g_cu_count[device].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+template <class S>
+hipError_t launch_gemm(const float* x, const float* w, const int32_t* offsets, float* y,
+                       int experts, int dense_rows, int K, int N, long tile_bound,
+                       hipStream_t stream) {
+  const bool vec = (K % 4 == 0) && (N % 4 == 0) && aligned16(x) && aligned16(w);
+  const long cap = static_cast<long>(device_cu_count()) * 2;
+  long grid = tile_bound < cap ? tile_bound : cap;
+  if (grid >= kXcds) grid = grid / kXcds * kXcds;
+  if (grid < 1) grid = 1;
+  const std::size_t lds = 2 * S::kStageFloats * sizeof(float) +
+                          2 * static_cast<std::size_t>(experts + 1) * sizeof(int32_t);
+  if (vec) {
+    rr_gemm_mfma_kernel<S, true><<<static_cast<unsigned>(grid), S::kThreads, lds, stream>>>(
+        x, w, offsets, y, experts, dense_rows, K, N);
+  } else {
+    rr_gemm_mfma_kernel<S, false><<<static_cast<unsigned>(grid), S::kThreads, lds, stream>>>(
+        x, w, offsets, y, experts, dense_rows, K, N);
+  }
+  return hipGetLastError();
+}
+
+using TileLarge = TileShape<128, 128, 2, 2>;  // 4 waves, 64x64 per wave
+using TileSmall = TileShape<64, 64, 2, 2>;    // 4 waves, 32x32 per wave
+
+long ceil_div(long a, long b) { return (a + b - 1) / b; }
+
+// Upper bound on the tile count given a per-expert row bound.
+long tile_bound(int experts, long rows_per_expert, int bm, int n, int bn) {
+  return static_cast<long>(experts) * ceil_div(rows_per_expert, bm) * ceil_div(n, bn);
+}
+
+hipError_t gemm_dispatch(const float* x, const float* w, const int32_t* offsets, float* y,
+                         int experts, int dense_rows, int K, int N, long rows_per_expert,
+                         long total_rows_estimate, hipStream_t stream) {
+  const long cus = device_cu_count();
+  // Prefer the 128x128 tile when it still yields two tiles per CU.
+  const long large_tiles =
+      (ceil_div(total_rows_estimate, TileLarge::BM) + (offsets ? experts : 0)) *
+      ceil_div(N, TileLarge::BN);
+  if (large_tiles >= 2 * cus) {
+    return launch_gemm<TileLarge>(x, w, offsets, y, experts, dense_rows, K, N,
+                                  tile_bound(experts, rows_per_expert, TileLarge::BM, N,
+                                             TileLarge::BN),
+                                  stream);
+  }
+  return launch_gemm<TileSmall>(x, w, offsets, y, experts, dense_rows, K, N,
+                                tile_bound(experts, rows_per_expert, TileSmall::BM, N,
+                                           TileSmall::BN),
+                                stream);
+}
+
+}  // namespace
+
+hipError_t dense_gemm_mfma(const float* a, const float* b, float* c, int m, int n, int k,
+                           hipStream_t stream) {
+  if (m <= 0 || n <= 0) return hipSuccess;
+  return gemm_dispatch(a, b, nullptr, c, 1, m, k, n, m, m, stream);
+}
+
+hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offsets, float* y,
+                             int experts, int hidden, int output, int max_expert_tokens,
+                             hipStream_t stream) {
+  if (max_expert_tokens <= 0 || output <= 0) return hipSuccess;
+  // The host never reads offsets; the caller's bound sizes the grid and the
+  // device scheduler covers every row of every segment.
+  const long total_estimate = max_expert_tokens;
+  return gemm_dispatch(x, w, offsets, y, experts, 0, hidden, output, max_expert_tokens,
+                       total_estimate, stream);
+}
+
+}  // namespace rr::kern

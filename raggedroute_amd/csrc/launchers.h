@@ -1,0 +1,69 @@
+// Host-side launchers of the gfx950 kernels (defined in the *.hip files).
+// Shapes are validated by the callers; every launcher returns the launch error.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rr::kern {
+
+// ---- dense / grouped GEMM on FP32 MFMA (gemm.hip) ----
+// c[m, n] = a[m, k] * b[k, n]
+hipError_t dense_gemm_mfma(const float* a, const float* b, float* c, int m, int n, int k,
+                           hipStream_t stream);
+// y[r, :] = x[r, :] * w[e] for r in [offsets[e], offsets[e + 1]); offsets read on device.
+hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offsets, float* y,
+                             int experts, int hidden, int output, int max_expert_tokens,
+                             hipStream_t stream);
+
+// ---- routing kernels (routing.hip) ----
+hipError_t topk_gate_wave(const float* logits, int32_t* ids, float* weights, int tokens,
+                          int experts, hipStream_t stream);
+// counts[e] = #{ids == e}; overwrites counts (no external reset needed).
+hipError_t histogram_native(const int32_t* ids, int32_t* counts, int route_pairs, int experts,
+                            hipStream_t stream);
+// offsets[0..E] exclusive prefix of counts; in-place safe (counts == offsets).
+hipError_t exclusive_scan_native(const int32_t* counts, int32_t* offsets, int experts,
+                                 hipStream_t stream);
+hipError_t histogram_exclusive_scan_native(const int32_t* ids, int32_t* counts, int32_t* offsets,
+                                           int route_pairs, int experts, hipStream_t stream);
+// Stable placement (route index ascending inside each expert segment) and
+// token-owned row copy; cursors end equal to the per-expert route counts.
+hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_t* offsets,
+                                int32_t* cursors, float* x_permuted, int32_t* route_pos,
+                                int32_t* sorted_route, int tokens, int experts, int top_k,
+                                int hidden, hipStream_t stream);
+hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
+                            const float* route_weights, float* y, int tokens, int top_k,
+                            int output, hipStream_t stream);
+
+// ---- naive baselines (naive.hip): reference semantics, no resets ----
+hipError_t dense_gemm_naive(const float* a, const float* b, float* c, int m, int n, int k,
+                            hipStream_t stream);
+hipError_t topk_gate_naive(const float* logits, int32_t* ids, float* weights, int tokens,
+                           int experts, hipStream_t stream);
+hipError_t histogram_naive(const int32_t* ids, int32_t* counts, int route_pairs, int experts,
+                           hipStream_t stream);
+hipError_t exclusive_scan_naive(const int32_t* counts, int32_t* offsets, int experts,
+                                hipStream_t stream);
+hipError_t token_permute_naive(const float* x, const int32_t* ids, const int32_t* offsets,
+                               int32_t* cursors, float* x_permuted, int32_t* route_pos,
+                               int32_t* sorted_route, int tokens, int top_k, int hidden,
+                               hipStream_t stream);
+hipError_t grouped_gemm_naive(const float* x, const float* w, const int32_t* offsets, float* y,
+                              int experts, int hidden, int output, int max_expert_tokens,
+                              hipStream_t stream);
+hipError_t unpermute_naive(const float* y_permuted, const int32_t* route_pos,
+                           const float* route_weights, float* y, int tokens, int top_k,
+                           int output, hipStream_t stream);
+
+// ---- support (support.hip) ----
+hipError_t cache_scrub(uint32_t* buffer, std::size_t elements, hipStream_t stream);
+hipError_t fill_uniform(float* out, std::size_t count, uint64_t seed, uint64_t stream_id,
+                        float low, float high, hipStream_t stream);
+hipError_t fill_normal(float* out, std::size_t count, uint64_t seed, uint64_t stream_id,
+                       float mean, float stddev, hipStream_t stream);
+
+}  // namespace rr::kern

@@ -1,0 +1,591 @@
+// gfx950 routing kernels: top-2 gate, histogram / exclusive scan / fused
+// histogram+scan, stable token permute, and the weighted unpermute.
+//
+// All of them are HBM- or launch-bound integer/byte work; they use wave64
+// ballots, LDS privatisation and 128-bit global accesses, never MFMA.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+#include "launchers.h"
+#include "raggedroute_capi.h"
+#include "wave.h"
+
+namespace rr::kern {
+namespace {
+
+using rr::dev::bits_for;
+using rr::dev::lane_id;
+using rr::dev::lanemask_lt;
+using rr::dev::match_mask;
+using rr::dev::wave_inclusive_scan;
+
+constexpr int kBlock = 1024;  // 16 waves
+constexpr int kWavesPerBlock = kBlock / 64;
+// Route counts up to this size take the single-workgroup metadata kernels.
+constexpr int kSingleBlockRoutes = 65536;
+
+// ============================================================================
+// Top-2 gate: selected softmax over the two largest logits of each row.
+// Semantics of reference src/topk_gate/cuda_naive/baseline.cu:18-80: order by
+// (value desc, expert asc); NaN ranks as -Inf; -0 and +0 tie (lower id wins);
+// equal selected values -> {0.5, 0.5}; +Inf first or -Inf second -> {1, 0};
+// else r = exp(v2 - v1), w1 = 1 / (1 + r), w2 = r * w1. An all-NaN row
+// therefore yields ids {0, 1} with weights {0.5, 0.5} without a special case.
+// ============================================================================
+
+// Packed key: larger key = better candidate. High word: order-preserving bits
+// of the value (NaN -> -Inf, -0 -> +0); low word: ~expert so ties prefer the
+// lower expert id. A zero key is below every real key.
+__device__ __forceinline__ uint64_t gate_key(float value, int expert) {
+  uint32_t bits = __float_as_uint(isnan(value) ? -INFINITY : value);
+  if ((bits << 1) == 0u) bits = 0u;
+  const uint32_t ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (static_cast<uint64_t>(ordered) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(expert));
+}
+
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint32_t ordered = static_cast<uint32_t>(key >> 32);
+  const uint32_t bits = (ordered & 0x80000000u) ? (ordered & 0x7FFFFFFFu) : ~ordered;
+  return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ int key_expert(uint64_t key) {
+  return static_cast<int>(~static_cast<uint32_t>(key));
+}
+
+__device__ __forceinline__ void insert_key(uint64_t key, uint64_t& k1, uint64_t& k2) {
+  if (key > k1) {
+    k2 = k1;
+    k1 = key;
+  } else if (key > k2) {
+    k2 = key;
+  }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+  const int lo = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), mask, 64);
+  const int hi = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), mask, 64);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+// LPR lanes cooperate on one row (LPR in 1..64, a power of two); each lane
+// keeps a local top-2 and the row's lanes merge with an xor butterfly.
+template <int LPR, bool VEC4>
+__global__ __launch_bounds__(256) void rr_topk_gate_kernel(const float* __restrict__ logits,
+                                                           int32_t* __restrict__ ids,
+                                                           float* __restrict__ weights,
+                                                           int tokens, int experts) {
+  constexpr int kRowsPerWave = 64 / LPR;
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int sub = lane % LPR;
+  const long row = (static_cast<long>(blockIdx.x) * 4 + wave) * kRowsPerWave + lane / LPR;
+  uint64_t k1 = 0, k2 = 0;
+  if (row < tokens) {
+    const float* p = logits + row * experts;
+    if (VEC4) {
+      const int quads = experts >> 2;
+      for (int q = sub; q < quads; q += LPR) {
+        const float4 v = reinterpret_cast<const float4*>(p)[q];
+        insert_key(gate_key(v.x, 4 * q + 0), k1, k2);
+        insert_key(gate_key(v.y, 4 * q + 1), k1, k2);
+        insert_key(gate_key(v.z, 4 * q + 2), k1, k2);
+        insert_key(gate_key(v.w, 4 * q + 3), k1, k2);
+      }
+    } else {
+      for (int e = sub; e < experts; e += LPR) insert_key(gate_key(p[e], e), k1, k2);
+    }
+  }
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) {
+    const uint64_t o1 = shfl_xor_u64(k1, d);
+    const uint64_t o2 = shfl_xor_u64(k2, d);
+    const uint64_t hi = k1 > o1 ? k1 : o1;
+    const uint64_t lo = k1 > o1 ? o1 : k1;
+    const uint64_t m2 = k2 > o2 ? k2 : o2;
+    k2 = lo > m2 ? lo : m2;
+    k1 = hi;
+  }
+  if (sub == 0 && row < tokens) {
+    const float v1 = key_value(k1);
+    const float v2 = key_value(k2);
+    float w1, w2;
+    if (v1 == v2) {
+      w1 = 0.5F;
+      w2 = 0.5F;
+    } else if (v1 == INFINITY || v2 == -INFINITY) {
+      w1 = 1.0F;
+      w2 = 0.0F;
+    } else {
+      const float r = expf(v2 - v1);
+      w1 = 1.0F / (1.0F + r);
+      w2 = __fmul_rn(r, w1);
+    }
+    ids[2 * row] = key_expert(k1);
+    ids[2 * row + 1] = key_expert(k2);
+    weights[2 * row] = w1;
+    weights[2 * row + 1] = w2;
+  }
+}
+
+template <int LPR>
+hipError_t launch_gate(const float* logits, int32_t* ids, float* weights, int tokens, int experts,
+                       bool vec4, hipStream_t stream) {
+  constexpr int kRowsPerBlock = 4 * (64 / LPR);
+  const unsigned blocks = static_cast<unsigned>((tokens + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (vec4) {
+    rr_topk_gate_kernel<LPR, true><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts);
+  } else {
+    rr_topk_gate_kernel<LPR, false><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts);
+  }
+  return hipGetLastError();
+}
+
+// ============================================================================
+// Histogram / exclusive scan.
+// ============================================================================
+
+// Counts the valid ids of routes [begin, end) into an LDS row with one
+// aggregated add per distinct id per 64 routes (ballot match), which keeps a
+// hot expert from serialising the wave. Rows may be shared by several waves,
+// hence the LDS atomic. Loads are batched 8 deep to keep them in flight.
+__device__ __forceinline__ void wave_count_ids(int32_t* row, const int32_t* __restrict__ ids,
+                                               int begin, int end, int experts, int bits,
+                                               int wave, int waves) {
+  constexpr int kBatch = 8;
+  const int lane = lane_id();
+  const int stride = waves * 64;
+  for (int base = begin + wave * 64; base < end; base += stride * kBatch) {
+    int32_t v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int r = base + u * stride + lane;
+      v[u] = r < end ? ids[r] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool valid = v[u] >= 0 && v[u] < experts;
+      const uint64_t active = __ballot(valid);
+      if (active == 0) continue;  // wave-uniform
+      const uint64_t mask = match_mask(static_cast<uint32_t>(valid ? v[u] : 0), bits, active);
+      if (valid && (mask & lanemask_lt()) == 0) atomicAdd(row + v[u], __popcll(mask));
+    }
+  }
+}
+
+// Number of LDS histogram rows: one per wave while 16 rows fit in 32 KB.
+__host__ __device__ __forceinline__ int private_rows(int experts) {
+  return experts <= 512 ? kWavesPerBlock : kWavesPerBlock / 2;
+}
+
+// Exclusive scan of one value per thread across a 1024-thread block.
+// wsum holds kWavesPerBlock ints of LDS. Returns the exclusive prefix and the
+// block total (wrapping int32 sums, as in the reference).
+__device__ __forceinline__ int32_t block_exclusive_scan(int32_t v, int32_t* wsum, int32_t* total) {
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int32_t x = wave_inclusive_scan(v);
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int32_t s = lane < kWavesPerBlock ? wsum[lane] : 0;
+    s = wave_inclusive_scan(s);
+    if (lane < kWavesPerBlock) wsum[lane] = s;
+  }
+  __syncthreads();
+  const int32_t before = wave > 0 ? wsum[wave - 1] : 0;
+  *total = wsum[kWavesPerBlock - 1];
+  return static_cast<int32_t>(static_cast<uint32_t>(before) + static_cast<uint32_t>(x) -
+                              static_cast<uint32_t>(v));
+}
+
+// Single workgroup: ids -> counts (and offsets when offsets != nullptr).
+// Overwrites counts, so no external reset is needed.
+__global__ __launch_bounds__(kBlock) void rr_hist_scan_single_kernel(
+    const int32_t* __restrict__ ids, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int routes, int experts, int bits) {
+  extern __shared__ int32_t lds[];
+  const int rows = private_rows(experts);
+  int32_t* bins = lds;                   // [rows][experts]
+  int32_t* wsum = lds + rows * experts;  // [16]
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid >> 6;
+  for (int i = tid; i < rows * experts; i += kBlock) bins[i] = 0;
+  __syncthreads();
+  wave_count_ids(bins + (wave % rows) * experts, ids, 0, routes, experts, bits, wave,
+                 kWavesPerBlock);
+  __syncthreads();
+  // experts <= kBlock: thread e owns expert e.
+  int32_t c = 0;
+  if (tid < experts) {
+    for (int w = 0; w < rows; ++w) c += bins[w * experts + tid];
+    counts[tid] = c;
+  }
+  if (offsets != nullptr) {
+    int32_t total = 0;
+    const int32_t excl = block_exclusive_scan(c, wsum, &total);
+    if (tid < experts) offsets[tid] = excl;
+    if (tid == 0) offsets[experts] = total;
+  }
+}
+
+// Multi-workgroup histogram: each block privatises its slice in LDS and merges
+// one atomic per non-zero expert into counts (which the host zeroed).
+__global__ __launch_bounds__(kBlock) void rr_hist_multi_kernel(const int32_t* __restrict__ ids,
+                                                               int32_t* counts, int routes,
+                                                               int experts, int bits, int chunk) {
+  extern __shared__ int32_t lds[];
+  const int rows = private_rows(experts);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid >> 6;
+  for (int i = tid; i < rows * experts; i += kBlock) lds[i] = 0;
+  __syncthreads();
+  const long begin = static_cast<long>(blockIdx.x) * chunk;
+  const long end = begin + chunk < routes ? begin + chunk : routes;
+  wave_count_ids(lds + (wave % rows) * experts, ids, static_cast<int>(begin),
+                 static_cast<int>(end), experts, bits, wave, kWavesPerBlock);
+  __syncthreads();
+  for (int e = tid; e < experts; e += kBlock) {
+    int32_t c = 0;
+    for (int w = 0; w < rows; ++w) c += lds[w * experts + e];
+    if (c != 0) atomicAdd(counts + e, c);
+  }
+}
+
+// Single workgroup exclusive scan; every count is read before any offset is
+// written, so counts and offsets may alias (in-place scan).
+__global__ __launch_bounds__(kBlock) void rr_scan_kernel(const int32_t* counts, int32_t* offsets,
+                                                         int experts) {
+  __shared__ int32_t wsum[kWavesPerBlock];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int32_t v = tid < experts ? counts[tid] : 0;
+  int32_t total = 0;
+  const int32_t excl = block_exclusive_scan(v, wsum, &total);  // contains __syncthreads
+  if (tid < experts) offsets[tid] = excl;
+  if (tid == 0) offsets[experts] = total;
+}
+
+// E == 1: every valid route belongs to expert 0, so counts[0] = routes without
+// reading the ids (same O(1) path as the reference's single-bin kernel).
+__global__ void rr_single_bin_kernel(int32_t* counts, int32_t* offsets, int routes) {
+  counts[0] = routes;
+  if (offsets != nullptr) {
+    offsets[0] = 0;
+    offsets[1] = routes;
+  }
+}
+
+std::size_t bins_bytes(int experts) {
+  return (static_cast<std::size_t>(private_rows(experts)) * experts + kWavesPerBlock) *
+         sizeof(int32_t);
+}
+
+hipError_t histogram_large(const int32_t* ids, int32_t* counts, int routes, int experts,
+                           hipStream_t stream) {
+  hipError_t err =
+      hipMemsetAsync(counts, 0, static_cast<std::size_t>(experts) * sizeof(int32_t), stream);
+  if (err != hipSuccess) return err;
+  // ~8 routes per thread per block, at most 128 blocks so that each counter
+  // sees a bounded number of global atomics.
+  int blocks = (routes + kBlock * 8 - 1) / (kBlock * 8);
+  if (blocks > 128) blocks = 128;
+  int chunk = (routes + blocks - 1) / blocks;
+  chunk = (chunk + 63) / 64 * 64;
+  blocks = (routes + chunk - 1) / chunk;
+  rr_hist_multi_kernel<<<blocks, kBlock, bins_bytes(experts), stream>>>(ids, counts, routes,
+                                                                       experts, bits_for(experts),
+                                                                       chunk);
+  return hipGetLastError();
+}
+
+// ============================================================================
+// Stable token permute.
+// route_pos[r] = offsets[e] + #{r' < r : ids[r'] == e} (route index ascending
+// inside each expert segment), the closed form of the reference's stable map
+// generator (reference benchmarks/adapters/unpermute_adapter.cpp:47-53).
+// Kernel 1 ranks the routes; kernel 2 copies token rows (x read once, written
+// top_k times).
+// ============================================================================
+
+// Block b ranks routes [b*chunk, (b+1)*chunk). It first counts every earlier
+// route per expert (a recomputed prefix: no inter-block communication and no
+// global scratch), then ranks its own routes WAVES*64 at a time: ballot-match
+// gives the rank inside a wave and per-wave counts, an LDS pass turns those
+// into the per-wave exclusive prefix of every expert. LDS: (WAVES + 1) * E ints.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void rr_permute_rank_kernel(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ offsets, int32_t* cursors,
+    int32_t* __restrict__ route_pos, int32_t* __restrict__ sorted_route, int routes, int experts,
+    int bits, int chunk) {
+  constexpr int kThreads = WAVES * 64;
+  extern __shared__ int32_t lds[];
+  int32_t* wc = lds;                      // [WAVES][experts]
+  int32_t* base = lds + WAVES * experts;  // [experts]
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid >> 6;
+  const int begin = static_cast<int>(blockIdx.x) * chunk;
+  const int end = begin + chunk < routes ? begin + chunk : routes;
+
+  for (int i = tid; i < WAVES * experts; i += kThreads) wc[i] = 0;
+  __syncthreads();
+  wave_count_ids(wc + wave * experts, ids, 0, begin, experts, bits, wave, WAVES);
+  __syncthreads();
+  for (int e = tid; e < experts; e += kThreads) {
+    int32_t s = 0;
+    for (int w = 0; w < WAVES; ++w) {
+      s += wc[w * experts + e];
+      wc[w * experts + e] = 0;
+    }
+    base[e] = s;
+  }
+  __syncthreads();
+
+  for (int sub = begin; sub < end; sub += kThreads) {
+    const int r = sub + tid;
+    const int id = r < end ? ids[r] : -1;
+    const bool valid = id >= 0 && id < experts;
+    const uint64_t active = __ballot(valid);
+    const uint64_t mask = match_mask(static_cast<uint32_t>(valid ? id : 0), bits, active);
+    const int rank = __popcll(mask & lanemask_lt());
+    const bool leader = valid && rank == 0;
+    if (leader) wc[wave * experts + id] = __popcll(mask);
+    __syncthreads();
+    // Per expert: replace each wave's count by the number of earlier routes of
+    // that expert (base plus earlier waves); untouched entries stay zero.
+    for (int e = tid; e < experts; e += kThreads) {
+      int32_t running = base[e];
+      for (int w = 0; w < WAVES; ++w) {
+        const int32_t c = wc[w * experts + e];
+        if (c != 0) {
+          wc[w * experts + e] = running;
+          running += c;
+        }
+      }
+      base[e] = running;
+    }
+    __syncthreads();
+    if (r < end) {
+      int32_t pos = -1;
+      if (valid) {
+        pos = offsets[id] + wc[wave * experts + id] + rank;
+        if (pos < 0 || pos >= routes) pos = -1;  // offsets inconsistent with ids
+      }
+      route_pos[r] = pos;
+      if (sorted_route != nullptr && pos >= 0) sorted_route[pos] = r;
+    }
+    // Leaders restore their entry to zero; the wave's own reads above precede
+    // this store in program order, and other waves read only their own rows.
+    if (leader) wc[wave * experts + id] = 0;
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    __syncthreads();
+    // base now counts every route of the expert: the cursor value a per-route
+    // atomic placement would leave behind.
+    for (int e = tid; e < experts; e += kThreads) cursors[e] = base[e];
+  }
+}
+
+// Token-owned row copy: element (t, c) of x is read once and stored to every
+// valid destination row of token t. VEC4: c indexes float4 columns.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __restrict__ x,
+                                                              const int32_t* __restrict__ route_pos,
+                                                              float* __restrict__ x_permuted,
+                                                              int tokens, int top_k, int hidden,
+                                                              int routes) {
+  const uint32_t cols = VEC4 ? static_cast<uint32_t>(hidden) / 4 : static_cast<uint32_t>(hidden);
+  const uint32_t total = static_cast<uint32_t>(tokens) * cols;
+  const uint32_t stride = blockDim.x * gridDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint32_t t = i / cols;
+    const uint32_t c = i - t * cols;
+    if (VEC4) {
+      const float4 v = reinterpret_cast<const float4*>(x + static_cast<std::size_t>(t) * hidden)[c];
+      for (int j = 0; j < top_k; ++j) {
+        const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
+        if (pos >= 0 && pos < routes) {
+          reinterpret_cast<float4*>(x_permuted + static_cast<std::size_t>(pos) * hidden)[c] = v;
+        }
+      }
+    } else {
+      const float v = x[static_cast<std::size_t>(t) * hidden + c];
+      for (int j = 0; j < top_k; ++j) {
+        const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
+        if (pos >= 0 && pos < routes) x_permuted[static_cast<std::size_t>(pos) * hidden + c] = v;
+      }
+    }
+  }
+}
+
+// ============================================================================
+// Unpermute: y[t, :] = sum_j w[t*top_k + j] * y_permuted[route_pos[t*top_k + j], :]
+// accumulated in rank order with separately rounded multiply and add, the
+// operation order of the reference's FP32 loop (reference
+// benchmarks/adapters/unpermute_adapter.cpp:67-73).
+// ============================================================================
+template <bool VEC4>
+__global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restrict__ y_permuted,
+                                                           const int32_t* __restrict__ route_pos,
+                                                           const float* __restrict__ route_weights,
+                                                           float* __restrict__ y, int tokens,
+                                                           int top_k, int output) {
+  const uint32_t cols = VEC4 ? static_cast<uint32_t>(output) / 4 : static_cast<uint32_t>(output);
+  const uint32_t total = static_cast<uint32_t>(tokens) * cols;
+  const uint32_t stride = blockDim.x * gridDim.x;
+  const int routes = tokens * top_k;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint32_t t = i / cols;
+    const uint32_t c = i - t * cols;
+    if (VEC4) {
+      float4 acc = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+      for (int j = 0; j < top_k; ++j) {
+        const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
+        const int32_t pos = route_pos[route];
+        if (pos < 0 || pos >= routes) continue;
+        const float w = route_weights[route];
+        const float4 v =
+            reinterpret_cast<const float4*>(y_permuted + static_cast<std::size_t>(pos) * output)[c];
+        acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
+        acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
+        acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
+        acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
+      }
+      reinterpret_cast<float4*>(y + static_cast<std::size_t>(t) * output)[c] = acc;
+    } else {
+      float acc = 0.0F;
+      for (int j = 0; j < top_k; ++j) {
+        const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
+        const int32_t pos = route_pos[route];
+        if (pos < 0 || pos >= routes) continue;
+        acc = __fadd_rn(acc, __fmul_rn(route_weights[route],
+                                       y_permuted[static_cast<std::size_t>(pos) * output + c]));
+      }
+      y[static_cast<std::size_t>(t) * output + c] = acc;
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+unsigned stream_grid(uint64_t items) {
+  // Enough blocks to cover 256 CUs several times; grid-stride beyond that.
+  const uint64_t blocks = (items + 255) / 256;
+  return static_cast<unsigned>(blocks < 8192 ? (blocks == 0 ? 1 : blocks) : 8192);
+}
+
+}  // namespace
+
+hipError_t topk_gate_wave(const float* logits, int32_t* ids, float* weights, int tokens,
+                          int experts, hipStream_t stream) {
+  if (tokens <= 0) return hipSuccess;
+  const bool vec4 = (experts % 4 == 0) && aligned16(logits);
+  const int per_lane_units = vec4 ? experts / 4 : (experts + 3) / 4;
+  int lpr = 1;
+  while (lpr < per_lane_units && lpr < 64) lpr <<= 1;
+  switch (lpr) {
+    case 1: return launch_gate<1>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 2: return launch_gate<2>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 4: return launch_gate<4>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 8: return launch_gate<8>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 16: return launch_gate<16>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 32: return launch_gate<32>(logits, ids, weights, tokens, experts, vec4, stream);
+    default: return launch_gate<64>(logits, ids, weights, tokens, experts, vec4, stream);
+  }
+}
+
+hipError_t histogram_native(const int32_t* ids, int32_t* counts, int routes, int experts,
+                            hipStream_t stream) {
+  if (experts == 1) {
+    rr_single_bin_kernel<<<1, 1, 0, stream>>>(counts, nullptr, routes);
+    return hipGetLastError();
+  }
+  if (routes <= kSingleBlockRoutes) {
+    rr_hist_scan_single_kernel<<<1, kBlock, bins_bytes(experts), stream>>>(
+        ids, counts, nullptr, routes, experts, bits_for(experts));
+    return hipGetLastError();
+  }
+  return histogram_large(ids, counts, routes, experts, stream);
+}
+
+hipError_t exclusive_scan_native(const int32_t* counts, int32_t* offsets, int experts,
+                                 hipStream_t stream) {
+  rr_scan_kernel<<<1, kBlock, 0, stream>>>(counts, offsets, experts);
+  return hipGetLastError();
+}
+
+hipError_t histogram_exclusive_scan_native(const int32_t* ids, int32_t* counts, int32_t* offsets,
+                                           int routes, int experts, hipStream_t stream) {
+  if (experts == 1) {
+    rr_single_bin_kernel<<<1, 1, 0, stream>>>(counts, offsets, routes);
+    return hipGetLastError();
+  }
+  if (routes <= kSingleBlockRoutes) {
+    rr_hist_scan_single_kernel<<<1, kBlock, bins_bytes(experts), stream>>>(
+        ids, counts, offsets, routes, experts, bits_for(experts));
+    return hipGetLastError();
+  }
+  const hipError_t err = histogram_large(ids, counts, routes, experts, stream);
+  if (err != hipSuccess) return err;
+  rr_scan_kernel<<<1, kBlock, 0, stream>>>(counts, offsets, experts);
+  return hipGetLastError();
+}
+
+hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_t* offsets,
+                                int32_t* cursors, float* x_permuted, int32_t* route_pos,
+                                int32_t* sorted_route, int tokens, int experts, int top_k,
+                                int hidden, hipStream_t stream) {
+  const int routes = tokens * top_k;
+  if (routes <= 0) return hipSuccess;
+  // One sub-chunk per block up to 64 blocks; beyond that the chunk grows so the
+  // recomputed prefix stays bounded by 64 chunks. 16 waves while (16 + 1) LDS
+  // rows of E ints fit in 34 KB, else 8 waves.
+  const bool wide = experts > 512;
+  const int threads = wide ? 512 : 1024;
+  int chunk = threads;
+  if (routes > 64 * threads) chunk = ((routes + 63) / 64 + threads - 1) / threads * threads;
+  const int blocks = (routes + chunk - 1) / chunk;
+  const std::size_t lds = (static_cast<std::size_t>(threads / 64) + 1) * experts * sizeof(int32_t);
+  if (wide) {
+    rr_permute_rank_kernel<8><<<blocks, threads, lds, stream>>>(
+        ids, offsets, cursors, route_pos, sorted_route, routes, experts, bits_for(experts), chunk);
+  } else {
+    rr_permute_rank_kernel<16><<<blocks, threads, lds, stream>>>(
+        ids, offsets, cursors, route_pos, sorted_route, routes, experts, bits_for(experts), chunk);
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || hidden == 0) return err;
+  const bool vec4 = (hidden % 4 == 0) && aligned16(x) && aligned16(x_permuted);
+  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? hidden / 4 : hidden);
+  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
+  if (vec4) {
+    rr_permute_copy_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
+        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+  } else {
+    rr_permute_copy_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
+        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+  }
+  return hipGetLastError();
+}
+
+hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
+                            const float* route_weights, float* y, int tokens, int top_k,
+                            int output, hipStream_t stream) {
+  if (tokens <= 0 || output <= 0) return hipSuccess;
+  const bool vec4 = (output % 4 == 0) && aligned16(y_permuted) && aligned16(y);
+  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? output / 4 : output);
+  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
+  if (vec4) {
+    rr_unpermute_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
+        y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+  } else {
+    rr_unpermute_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
+        y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace rr::kern

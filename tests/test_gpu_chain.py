@@ -1,0 +1,178 @@
+"""Chain parity: chain_from_tokens / chain_from_logits on the gfx950 library
+against the reference chain oracle (reference
+benchmarks/adapters/chain_adapter.cpp:188-239, validate :469-495).
+
+Integer outputs are bit-exact: top-2 ids against the oracle top-2 applied to
+the device logits (chain_from_tokens: the MFMA router sums in a different
+order than the sequential CPU loop, so the logits themselves are checked
+against the accumulation-aware GEMM bound and rows whose CPU rank-2/rank-3
+margin lies inside that bound are counted as near-ties), counts, offsets and
+the stable route map. Weights within 1e-6 (reference chain tolerance), the
+final output within atol 1e-4 + rtol 4e-5*K (reference chain_adapter.cpp:492).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import raggedroute_amd as rr
+from raggedroute_amd import workloads
+from conftest import to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+U32 = 2.0 ** -24
+
+
+class ChainRun:
+    def __init__(self, cfg: workloads.ChainConfig, inputs: dict, device, kernel=None, with_inverse=True):
+        t, e, k, n = cfg.tokens, cfg.experts, cfg.hidden, cfg.output
+        self.cfg = cfg
+        dev = lambda a: a if isinstance(a, torch.Tensor) else to_dev(a, device)  # noqa: E731
+        self.x = dev(inputs["x"])
+        self.we = dev(inputs["expert_weights"])
+        self.wr = dev(inputs["router_weights"]) if cfg.from_tokens else None
+        self.logits = (torch.empty(t, e, device=device) if cfg.from_tokens
+                       else to_dev(inputs["logits"], device))
+        i32 = dict(dtype=torch.int32, device=device)
+        self.ids = torch.full((t, 2), -1, **i32)
+        self.w = torch.empty(t, 2, device=device)
+        self.counts = torch.full((e,), -1, **i32)
+        self.offsets = torch.full((e + 1,), -1, **i32)
+        self.xp = torch.empty(2 * t, k, device=device)
+        self.pos = torch.full((2 * t,), -1, **i32)
+        self.inv = torch.full((2 * t,), -1, **i32) if with_inverse else None
+        self.yp = torch.empty(2 * t, n, device=device)
+        self.y = torch.empty(t, n, device=device)
+        self.args = rr.ChainArgs(
+            x=self.x.data_ptr(), router_weights=self.wr.data_ptr() if self.wr is not None else None,
+            logits=self.logits.data_ptr(), expert_ids=self.ids.data_ptr(), route_weights=self.w.data_ptr(),
+            counts=self.counts.data_ptr(), offsets=self.offsets.data_ptr(), x_permuted=self.xp.data_ptr(),
+            route_pos=self.pos.data_ptr(), sorted_route=self.inv.data_ptr() if self.inv is not None else None,
+            expert_weights=self.we.data_ptr(), y_permuted=self.yp.data_ptr(), y=self.y.data_ptr(),
+            tokens=t, experts=e, hidden=k, output=n, kernel=kernel or rr.kernel())
+        self.ws = torch.empty(rr.get_chain_workspace_size(self.args) // 4, **i32)
+
+    def run(self, ctx):
+        c = rr.RuntimeContext(stream=ctx.stream, workspace=self.ws.data_ptr(),
+                              workspace_bytes=self.ws.numel() * 4, architecture=ctx.architecture)
+        fn = rr.chain_from_tokens if self.cfg.from_tokens else rr.chain_from_logits
+        status = fn(self.args, c)
+        assert status.ok(), status.message
+        torch.cuda.synchronize()
+        return {name: to_host(getattr(self, attr)) for name, attr in
+                [("logits", "logits"), ("ids", "ids"), ("weights", "w"), ("counts", "counts"),
+                 ("offsets", "offsets"), ("route_pos", "pos"), ("y", "y"), ("x_permuted", "xp"),
+                 ("y_permuted", "yp")]} | ({"sorted_route": to_host(self.inv)} if self.inv is not None else {})
+
+
+def logits_bound(x, wr):
+    """Per-element accumulation-aware bound 4*gamma_K*sum|x*w| + 1e-7."""
+    k = x.shape[1]
+    gamma = k * U32 / (1 - k * U32)
+    return 4 * gamma * (np.abs(x.astype(np.float64)) @ np.abs(wr.astype(np.float64))) + 1e-7
+
+
+def check_chain(cfg, inp, dev, sample_tokens=None):
+    t, e, k = cfg.tokens, cfg.experts, cfg.hidden
+    report = {}
+    if cfg.from_tokens:
+        rows = np.arange(t) if sample_tokens is None else sample_tokens
+        x_s = inp["x"][rows]
+        exact = oracle.dense_gemm_f64(x_s, inp["router_weights"])
+        err = np.abs(dev["logits"][rows].astype(np.float64) - exact)
+        bound = logits_bound(x_s, inp["router_weights"])
+        assert (err <= bound).all(), f"router logits exceed the GEMM bound (max ratio {(err / bound).max()})"
+        # near-tie rows: the CPU's 1st/2nd or 2nd/3rd logits closer than twice the bound
+        cpu_logits = oracle.dense_gemm_f32_seq(x_s, inp["router_weights"])
+        srt = np.sort(cpu_logits.astype(np.float64), axis=1)[:, ::-1]
+        margin = np.minimum(srt[:, 0] - srt[:, 1], srt[:, 1] - srt[:, 2])
+        near = margin <= 2 * bound.max(axis=1)
+        report["near_tie_rows"] = int(near.sum())
+        cpu_ids, _ = oracle.top2_f32(cpu_logits)
+        differ = (cpu_ids != dev["ids"][rows]).any(axis=1)
+        report["id_rows_differing_from_cpu_logits"] = int(differ.sum())
+        # ids may differ from the CPU-logit oracle only on near-tie rows
+        assert near[differ].all()
+        logits = dev["logits"]
+    else:
+        logits = inp["logits"]
+        assert np.array_equal(dev["logits"], logits)
+    ids, w = oracle.top2_f32(logits)
+    assert np.array_equal(dev["ids"], ids), "chain ids differ from the oracle top-2"
+    fails, max_abs, _ = oracle.compare_floating(dev["weights"], w, 1e-6, 1e-6)
+    assert fails == 0, f"chain weights: max |err| {max_abs}"
+    counts = oracle.histogram(ids, e)
+    offsets = oracle.exclusive_scan(counts)
+    assert np.array_equal(dev["counts"], counts) and np.array_equal(dev["offsets"], offsets)
+    pos = oracle.stable_route_pos(ids, offsets)
+    assert np.array_equal(dev["route_pos"], pos)
+    if "sorted_route" in dev:
+        assert np.array_equal(dev["sorted_route"], oracle.inverse_route(pos))
+    # final output: reference chain oracle on the device ids/weights
+    tok = np.arange(t) if sample_tokens is None else sample_tokens
+    y_exp = oracle.chain_output_f32(inp["x"][tok], inp["expert_weights"], ids[tok], w[tok])
+    fails, max_abs, max_rel = oracle.compare_floating(dev["y"][tok], y_exp, 1e-4, 4e-5 * k)
+    assert fails == 0, f"chain output: max |err| {max_abs}"
+    report["y_max_abs"] = max_abs
+    # x_permuted rows are bitwise copies (reference permute reference.cpp:65-71)
+    src = pos.reshape(t, 2)[tok]
+    assert np.array_equal(dev["x_permuted"][src[:, 0]].view(np.uint32), inp["x"][tok].view(np.uint32))
+    assert np.array_equal(dev["x_permuted"][src[:, 1]].view(np.uint32), inp["x"][tok].view(np.uint32))
+    return report
+
+
+@pytest.mark.parametrize("kernel_family", [rr.KernelFamily.kAuto, rr.KernelFamily.kNaive])
+def test_chain_tiny_shape(ctx, device, kernel_family):
+    # reference tests/correctness_tests.cpp:788-802 runs every chain at T5/E4/K7/N5
+    for from_tokens in (True, False):
+        cfg = workloads.ChainConfig("tiny", 5, 4, 7, 5, from_tokens=from_tokens)
+        inp = workloads.chain_inputs(cfg, seed=0)
+        dev = ChainRun(cfg, inp, device, rr.kernel(kernel_family)).run(ctx)
+        check_chain(cfg, inp, dev)
+
+
+@pytest.mark.parametrize("name", ["C1", "headline", "C2"])
+def test_chain_configs(ctx, device, name):
+    cfg = workloads.CHAIN_CONFIGS[name]
+    inp = workloads.chain_inputs(cfg, seed=0)
+    run = ChainRun(cfg, inp, device)
+    report = check_chain(cfg, inp, run.run(ctx))
+    print(f"{name}: {report}")
+    # repeated invocation on the same buffers is deterministic
+    again = run.run(ctx)
+    first = run.run(ctx)
+    for key in ("ids", "counts", "offsets", "route_pos", "y"):
+        assert np.array_equal(again[key], first[key])
+
+
+def test_chain_c5_sampled(ctx, device):
+    """C5 (T=16384, K=2048, E=128, N=768): integer outputs in full, floats on a
+    seeded sample of 192 tokens (the full FP32 CPU chain is ~52 GMAC)."""
+    cfg = workloads.C5
+    inp_dev = workloads.chain_inputs_device(cfg, 0, device)
+    dev = ChainRun(cfg, inp_dev, device, with_inverse=False).run(ctx)
+    inp = {key: to_host(v) for key, v in inp_dev.items()}
+    sample = np.sort(workloads.seeded_permutation(cfg.tokens, 0, 77)[:192])
+    report = check_chain(cfg, inp, dev, sample_tokens=sample)
+    print(f"C5: {report}")
+
+
+def test_chain_from_logits_route_trace(ctx, device, kat):
+    """chain_from_logits driven by the reference route-trace fixture: logits
+    -8 everywhere, +2 / +1 at the desired ids (reference chain_adapter.cpp:209-230)."""
+    raw = kat.raw["route_trace_fixture"]
+    t, e = raw["tokens"], raw["experts"]
+    for frame, desired in raw["frames"].items():
+        desired = np.array(desired, np.int32).reshape(t, 2)
+        logits = np.full((t, e), -8.0, np.float32)
+        logits[np.arange(t), desired[:, 0]] = 2.0
+        logits[np.arange(t), desired[:, 1]] = 1.0
+        cfg = workloads.ChainConfig("trace", t, e, 16, 8, from_tokens=False)
+        inp = workloads.chain_inputs(cfg, seed=1)
+        inp["logits"] = logits
+        dev = ChainRun(cfg, inp, device).run(ctx)
+        assert np.array_equal(dev["ids"], desired), frame
+        check_chain(cfg, inp, dev)

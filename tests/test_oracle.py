@@ -1,0 +1,389 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Each oracle function is checked against the reference's own known-answer
+vectors (tests/golden/kat.json), against closed forms / library routines
+(numpy bincount, cumsum, stable argsort, float64 matmul) and brute force on
+small inputs, and with planted mistakes that the comparison helpers must catch.
+CPU only.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+NAN, INF = math.nan, math.inf
+
+
+# ----------------------------------------------------------------- dense GEMM
+
+def test_dense_gemm_kat(kat):
+    a, b, c = (np.array(kat("dense_gemm_2x2", f)) for f in ("a", "b", "c"))
+    assert np.array_equal(oracle.dense_gemm_f64(a, b), c)
+    assert np.array_equal(oracle.dense_gemm_f32_seq(a, b), c.astype(np.float32))
+
+
+def test_dense_gemm_matches_numpy_f64():
+    rng = np.random.default_rng(1)
+    a, b = rng.standard_normal((17, 13)), rng.standard_normal((13, 19))
+    np.testing.assert_allclose(oracle.dense_gemm_f64(a, b), a @ b, rtol=1e-13, atol=1e-13)
+
+
+def test_dense_gemm_f32_is_sequential_rounded_sum():
+    # Brute force on a tiny case: acc = fl(acc + fl(a*b)) in k order.
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((3, 9)).astype(np.float32)
+    b = rng.standard_normal((9, 4)).astype(np.float32)
+    expect = np.zeros((3, 4), np.float32)
+    for i in range(3):
+        for j in range(4):
+            acc = np.float32(0)
+            for p in range(9):
+                acc = np.float32(acc + np.float32(a[i, p] * b[p, j]))
+            expect[i, j] = acc
+    assert np.array_equal(oracle.dense_gemm_f32_seq(a, b), expect)
+
+
+def test_dense_gemm_k0_writes_zeros(kat):
+    case = kat("zero_size_contract", "dense_k0")
+    c = oracle.dense_gemm_f64(np.zeros((case["m"], 0)), np.zeros((0, case["n"])))
+    assert np.array_equal(c.reshape(-1), case["c"])
+
+
+# ------------------------------------------------------------------- top-2 gate
+
+@pytest.mark.parametrize("name", ["topk_gate_3x4", "topk_all_nan_1x3", "topk_infinity_1x3"])
+def test_top2_kats(kat, name):
+    logits = np.array(kat(name, "logits"))
+    for fn in (oracle.top2_f32, oracle.top2_f64):
+        ids, w = fn(logits)
+        assert ids.tolist() == kat(name, "ids")
+        assert w.tolist() == kat(name, "weights")
+
+
+def brute_top2(row):
+    """Sort-based top-2 under (value desc, id asc) with NaN as -Inf."""
+    vals = [(-INF if math.isnan(v) else float(v)) for v in row]
+    order = sorted(range(len(vals)), key=lambda e: (-vals[e], e))
+    e1, e2 = order[0], order[1]
+    v1, v2 = vals[e1], vals[e2]
+    if v1 == v2:
+        w = (0.5, 0.5)
+    elif v1 == INF or v2 == -INF:
+        w = (1.0, 0.0)
+    else:
+        r = math.exp(v2 - v1)
+        w = (1.0 / (1.0 + r), r / (1.0 + r))
+    return (e1, e2), w
+
+
+def special_rows(mode: str, experts: int, rng):
+    """Input modes of reference benchmarks/adapters/topk_gate_adapter.cpp:208-249."""
+    row = rng.uniform(-1, 1, experts).astype(np.float32)
+    if mode == "ties":
+        row[:] = 1.0
+    elif mode == "all_nan":
+        row[:] = NAN
+    elif mode == "duplicate_max":
+        row[:] = -3.0; row[0] = 7.0; row[-1] = 7.0
+    elif mode == "signed_zero":
+        row = np.array([0.0 if e % 2 else -0.0 for e in range(experts)], np.float32)
+    elif mode == "mixed_nan_neg_inf":
+        row[:] = -INF; row[0] = NAN
+        if experts > 2:
+            row[2] = NAN
+    elif mode == "single_infinity":
+        row[-1] = INF
+    elif mode == "multiple_infinity":
+        row[0] = INF; row[-1] = INF
+    elif mode == "extreme":
+        row[:] = -1.0e30; row[0] = 1.0e30; row[1] = 0.0
+    return row
+
+
+SPECIAL_EXPECT = {
+    "ties": lambda e: ((0, 1), (0.5, 0.5)),
+    "all_nan": lambda e: ((0, 1), (0.5, 0.5)),
+    "duplicate_max": lambda e: ((0, e - 1), (0.5, 0.5)),
+    "signed_zero": lambda e: ((0, 1), (0.5, 0.5)),
+    "mixed_nan_neg_inf": lambda e: ((0, 1), (0.5, 0.5)),
+    "multiple_infinity": lambda e: ((0, e - 1), (0.5, 0.5)),
+    "extreme": lambda e: ((0, 1), (1.0, 0.0)),
+}
+
+
+@pytest.mark.parametrize("experts", [2, 3, 4, 7, 8, 16, 33, 64, 128])
+@pytest.mark.parametrize("mode", sorted(SPECIAL_EXPECT) + ["single_infinity"])
+def test_top2_special_modes(mode, experts):
+    rng = np.random.default_rng(experts)
+    rows = np.stack([special_rows(mode, experts, rng) for _ in range(3)])
+    ids, w = oracle.top2_f32(rows)
+    for t in range(3):
+        if mode == "single_infinity":
+            (e1, e2), ww = brute_top2(rows[t])
+            assert e1 == experts - 1 and ww == (1.0, 0.0)
+            expect_ids, expect_w = (e1, e2), ww
+        else:
+            expect_ids, expect_w = SPECIAL_EXPECT[mode](experts)
+        assert tuple(ids[t]) == expect_ids
+        assert tuple(float(x) for x in w[t]) == expect_w
+
+
+@pytest.mark.parametrize("experts", [2, 3, 5, 8, 13, 64])
+def test_top2_brute_force(experts):
+    rng = np.random.default_rng(100 + experts)
+    tokens = 200
+    # Small integer grid -> many exact ties; sprinkle NaN, +-Inf and signed zeros.
+    logits = rng.integers(-3, 4, (tokens, experts)).astype(np.float32)
+    mask = rng.random((tokens, experts))
+    logits[mask < 0.05] = NAN
+    logits[(mask >= 0.05) & (mask < 0.07)] = INF
+    logits[(mask >= 0.07) & (mask < 0.09)] = -INF
+    logits[(mask >= 0.09) & (mask < 0.12)] = -0.0
+    ids32, w32 = oracle.top2_f32(logits)
+    ids64, w64 = oracle.top2_f64(logits.astype(np.float64))
+    for t in range(tokens):
+        e, w = brute_top2(logits[t])
+        assert tuple(ids32[t]) == e and tuple(ids64[t]) == e
+        np.testing.assert_allclose(w64[t], w, rtol=1e-15, atol=0)
+        np.testing.assert_allclose(w32[t], w, rtol=1e-6, atol=1e-7)
+
+
+def test_top2_randomized_invariants():
+    # reference tests/correctness_framework_tests.cpp:295-321 (32 iterations)
+    rng = np.random.default_rng(20260729)
+    for it in range(32):
+        tokens, experts = 1 + it % 11, (4 if it % 2 == 0 else 8)
+        logits = rng.uniform(-2, 2, (tokens, experts))
+        ids, w = oracle.top2_f64(logits)
+        ids2, w2 = oracle.top2_f64(logits)
+        assert np.array_equal(ids, ids2) and np.array_equal(w, w2)
+        offsets = oracle.exclusive_scan(oracle.histogram(ids, experts))
+        assert offsets[-1] == ids.size
+        assert (ids[:, 0] != ids[:, 1]).all() and ids.min() >= 0 and ids.max() < experts
+        assert np.abs(w.sum(axis=1) - 1.0).max() < 1e-12
+
+
+# --------------------------------------------------------- histogram and scan
+
+def test_histogram_kat(kat):
+    counts = oracle.histogram(kat("histogram_reset", "ids"), 2)
+    assert counts.tolist() == kat("histogram_reset", "counts")
+    assert oracle.histogram(np.zeros(0, np.int32), 2).tolist() == kat("histogram_reset", "zero_route_counts")
+
+
+@pytest.mark.parametrize("experts", [1, 2, 33, 256, 1024])
+def test_histogram_matches_bincount(experts):
+    ids = np.random.default_rng(experts).integers(0, experts, 50_000).astype(np.int32)
+    assert np.array_equal(oracle.histogram(ids, experts), np.bincount(ids, minlength=experts))
+
+
+def test_histogram_rejects_out_of_range():
+    with pytest.raises(oracle.OracleError):
+        oracle.histogram(np.array([0, 2], np.int32), 2)
+    with pytest.raises(oracle.OracleError):
+        oracle.histogram(np.array([-1], np.int32), 2)
+
+
+@pytest.mark.parametrize("experts", [1, 31, 32, 33, 63, 64, 1024])
+def test_exclusive_scan_mod5(experts):
+    counts = np.arange(experts, dtype=np.int32) % 5
+    expect = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    assert np.array_equal(oracle.exclusive_scan(counts), expect)
+
+
+def test_exclusive_scan_int32_max(kat):
+    counts = np.zeros(64, np.int32)
+    counts[0] = kat("exclusive_scan_int32_max", "counts_first")
+    offsets = oracle.exclusive_scan(counts)
+    assert offsets[0] == 0 and (offsets[1:] == 2**31 - 1).all()
+    counts[1] = 1
+    with pytest.raises(oracle.OracleError):
+        oracle.exclusive_scan(counts)
+    with pytest.raises(oracle.OracleError):
+        oracle.exclusive_scan(np.array([1, -1], np.int32))
+
+
+@pytest.mark.parametrize("routes,experts", [(0, 1), (1, 8), (257, 33), (4096, 64), (4097, 64)])
+def test_fused_round_robin(routes, experts):
+    # reference tests/operator_api_tests.cpp:442-491
+    ids = (np.arange(routes) % experts).astype(np.int32)
+    counts = oracle.histogram(ids, experts)
+    expect = np.array([len(range(e, routes, experts)) for e in range(experts)])
+    assert np.array_equal(counts, expect)
+    assert np.array_equal(oracle.exclusive_scan(counts)[1:], np.cumsum(expect))
+
+
+# -------------------------------------------------------------------- permute
+
+def test_stable_permute_kat(kat):
+    g = lambda f: kat("routing_framework", f)  # noqa: E731
+    offsets = oracle.exclusive_scan(oracle.histogram(g("ids"), g("experts")))
+    assert offsets.tolist() == g("offsets")
+    pos = oracle.stable_route_pos(g("ids"), offsets)
+    assert pos.tolist() == g("route_pos")
+    assert oracle.inverse_route(pos).tolist() == g("sorted_route")
+    xp = oracle.permute_rows(np.array(g("x")), pos, g("top_k"))
+    assert xp.tolist() == g("x_permuted")
+    assert oracle.validate_permute(np.array(g("x")), g("ids"), offsets, xp, pos,
+                                   np.array(g("sorted_route")), g("top_k")) == []
+
+
+@pytest.mark.parametrize("experts", [1, 2, 8, 64, 1024])
+def test_stable_permute_is_stable_argsort(experts):
+    rng = np.random.default_rng(experts)
+    ids = rng.integers(0, experts, 6000).astype(np.int32)
+    offsets = oracle.exclusive_scan(oracle.histogram(ids, experts))
+    pos = oracle.stable_route_pos(ids, offsets)
+    # closed form: the route ranked k-th by a stable sort on the id lands at k
+    expect = np.empty_like(pos)
+    expect[np.argsort(ids, kind="stable")] = np.arange(ids.size)
+    assert np.array_equal(pos, expect)
+
+
+def test_validate_permute_catches_planted_mistakes():
+    rng = np.random.default_rng(5)
+    tokens, top_k, hidden, experts = 50, 2, 6, 4
+    ids = np.stack([rng.permutation(experts)[:2] for _ in range(tokens)]).astype(np.int32)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    offsets = oracle.exclusive_scan(oracle.histogram(ids, experts))
+    pos = oracle.stable_route_pos(ids, offsets)
+    xp = oracle.permute_rows(x, pos, top_k)
+    inv = oracle.inverse_route(pos)
+    assert oracle.validate_permute(x, ids, offsets, xp, pos, inv, top_k) == []
+    # swap two routes of different experts -> segment failure
+    a = 0
+    b = int(np.nonzero(ids.reshape(-1) != ids.reshape(-1)[0])[0][0])
+    bad = pos.copy(); bad[a], bad[b] = bad[b], bad[a]
+    assert "expert_segment" in oracle.validate_permute(x, ids, offsets, xp, bad, None, top_k)
+    dup = pos.copy(); dup[1] = dup[0]
+    assert "bijection" in oracle.validate_permute(x, ids, offsets, xp, dup, None, top_k)
+    wrong = xp.copy(); wrong[pos[3], 0] += 1.0
+    assert "row_copy" in oracle.validate_permute(x, ids, offsets, wrong, pos, None, top_k)
+    inv_bad = inv.copy(); inv_bad[0], inv_bad[1] = inv_bad[1], inv_bad[0]
+    assert "inverse_mapping" in oracle.validate_permute(x, ids, offsets, xp, pos, inv_bad, top_k)
+
+
+# --------------------------------------------------------------- grouped GEMM
+
+def test_grouped_gemm_kat(kat):
+    g = lambda f: np.array(kat("grouped_unpermute_framework", f))  # noqa: E731
+    yp = oracle.grouped_gemm_f64(g("x_permuted"), g("weights"), g("offsets").astype(np.int32))
+    assert np.array_equal(yp, g("y_permuted"))
+    y = oracle.unpermute_f64(yp, g("route_pos"), g("route_weights"), 2)
+    assert np.array_equal(y, g("y"))
+
+
+def test_grouped_gemm_matches_segment_matmul():
+    rng = np.random.default_rng(9)
+    experts, hidden, output = 5, 33, 17
+    counts = np.array([7, 0, 12, 1, 0], np.int32)
+    offsets = oracle.exclusive_scan(counts)
+    x = rng.standard_normal((offsets[-1], hidden))
+    w = rng.standard_normal((experts, hidden, output))
+    y = oracle.grouped_gemm_f64(x, w, offsets)
+    for e in range(experts):
+        s, t = offsets[e], offsets[e + 1]
+        np.testing.assert_allclose(y[s:t], x[s:t] @ w[e], rtol=1e-12, atol=1e-12)
+    y32 = oracle.grouped_gemm_f32_seq(x.astype(np.float32), w.astype(np.float32), offsets)
+    fails, _, _ = oracle.compare_gemm(y32[0:7], y[0:7], x[0:7], w[0])
+    assert fails == 0
+
+
+def test_grouped_gemm_k0(kat):
+    case = kat("zero_size_contract", "grouped_k0")
+    offsets = np.array(case["offsets"], np.int32)
+    y = oracle.grouped_gemm_f64(np.zeros((2, 0)), np.zeros((1, 0, 2)), offsets)
+    assert y.reshape(-1).tolist() == case["y"]
+
+
+# ------------------------------------------------------------------ unpermute
+
+def test_unpermute_kat(kat):
+    g = lambda f: kat("unpermute_weighted", f)  # noqa: E731
+    yp = np.repeat(np.arange(1, 5, dtype=np.float32)[:, None], g("width"), axis=1)
+    for fn in (oracle.unpermute_f32, oracle.unpermute_f64):
+        y = fn(yp, g("route_pos"), g("route_weights"), 2)
+        assert np.abs(y[0] - g("y")[0]).max() <= g("atol")
+        assert np.abs(y[1] - g("y")[1]).max() <= g("atol")
+
+
+def test_unpermute_closed_form():
+    rng = np.random.default_rng(11)
+    tokens, top_k, output = 40, 3, 9
+    yp = rng.standard_normal((tokens * top_k, output)).astype(np.float32)
+    pos = rng.permutation(tokens * top_k).astype(np.int32)
+    w = rng.uniform(0.05, 1, tokens * top_k).astype(np.float32)
+    y64 = oracle.unpermute_f64(yp, pos, w, top_k)
+    expect = (w[:, None].astype(np.float64) * yp[pos].astype(np.float64)).reshape(tokens, top_k, output).sum(1)
+    np.testing.assert_allclose(y64, expect, rtol=1e-12, atol=1e-12)
+    # FP32 loop: acc = fl(acc + fl(w*v)) in rank order
+    acc = np.zeros((tokens, output), np.float32)
+    for j in range(top_k):
+        r = np.arange(tokens) * top_k + j
+        acc = (acc + (w[r][:, None] * yp[pos[r]]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(oracle.unpermute_f32(yp, pos, w, top_k), acc)
+
+
+# ---------------------------------------------------------------- comparisons
+
+def test_compare_floating_detects_mismatch():
+    # reference tests/correctness_framework_tests.cpp:202-206
+    assert oracle.compare_floating([1.0], [2.0], 0.0, 0.0)[0] == 1
+    assert oracle.compare_floating([1.0], [1.0], 0.0, 0.0)[0] == 0
+    assert oracle.compare_floating([NAN], [1.0], 1.0, 1.0)[0] == 1      # class mismatch
+    assert oracle.compare_floating([INF], [-INF], 1.0, 1.0)[0] == 1
+    assert oracle.compare_floating([NAN, INF], [NAN, INF], 0.0, 0.0)[0] == 0
+    # allowed = atol + rtol * |e|
+    assert oracle.compare_floating([1.0 + 1.9e-6], [1.0], 1e-6, 1e-6)[0] == 0
+    assert oracle.compare_floating([1.0 + 3e-6], [1.0], 1e-6, 1e-6)[0] == 1
+
+
+def test_compare_gemm_bound_accepts_fp32_and_rejects_planted_error():
+    rng = np.random.default_rng(3)
+    m, n, k = 16, 12, 512
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    exact = oracle.dense_gemm_f64(a, b)
+    approx = oracle.dense_gemm_f32_seq(a, b).astype(np.float64)
+    fails, _, ratio = oracle.compare_gemm(approx, exact, a, b)
+    assert fails == 0 and ratio < 1.0
+    bound = 4 * (k * 2.0**-24 / (1 - k * 2.0**-24)) * (np.abs(a[0:1].astype(np.float64)).T * np.abs(b[:, 0:1])).sum() + 1e-7
+    bad = approx.copy(); bad[0, 0] += 1.5 * bound
+    assert oracle.compare_gemm(bad, exact, a, b)[0] == 1
+
+
+# -------------------------------------------------------------------- chain
+
+def test_chain_oracle_is_the_stage_composition():
+    from raggedroute_amd import workloads
+    cfg = workloads.ChainConfig("tiny", 5, 4, 7, 5)  # reference tests/correctness_tests.cpp:788-802 shape
+    inp = workloads.chain_inputs(cfg, seed=0)
+    out = oracle.chain(inp["x"], inp["expert_weights"], router_weights=inp["router_weights"])
+    logits = oracle.dense_gemm_f32_seq(inp["x"], inp["router_weights"])
+    assert np.array_equal(out["logits"], logits)
+    ids, w = oracle.top2_f32(logits)
+    assert np.array_equal(out["ids"], ids) and np.array_equal(out["weights"], w)
+    counts = oracle.histogram(ids, 4)
+    offsets = oracle.exclusive_scan(counts)
+    assert np.array_equal(out["counts"], counts) and np.array_equal(out["offsets"], offsets)
+    assert np.array_equal(out["route_pos"], oracle.stable_route_pos(ids, offsets))
+    # combined output against the float64 closed form sum_k w_k * (x @ W[e_k])
+    x64 = inp["x"].astype(np.float64); we = inp["expert_weights"].astype(np.float64)
+    expect = sum(w[:, j:j + 1] * np.einsum("th,tho->to", x64, we[ids[:, j]]) for j in range(2))
+    np.testing.assert_allclose(out["y"], expect, rtol=1e-5, atol=1e-6)
+
+
+def test_route_trace_fixture_metadata(kat):
+    raw = kat.raw["route_trace_fixture"]
+    for frame, ids in raw["frames"].items():
+        ids = np.array(ids, np.int32).reshape(raw["tokens"], raw["top_k"])
+        assert (ids[:, 0] != ids[:, 1]).all(), frame
+        counts = oracle.histogram(ids, raw["experts"])
+        assert counts.sum() == raw["tokens"] * raw["top_k"]
+        offsets = oracle.exclusive_scan(counts)
+        pos = oracle.stable_route_pos(ids, offsets)
+        assert sorted(pos.tolist()) == list(range(ids.size))
