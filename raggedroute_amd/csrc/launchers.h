@@ -48,10 +48,11 @@ hipError_t histogram_naive(const int32_t* ids, int32_t* counts, int route_pairs,
                            hipStream_t stream);
 hipError_t exclusive_scan_naive(const int32_t* counts, int32_t* offsets, int experts,
                                 hipStream_t stream);
+// experts bounds the ids used to index offsets (INT_MAX: trust the ids).
 hipError_t token_permute_naive(const float* x, const int32_t* ids, const int32_t* offsets,
                                int32_t* cursors, float* x_permuted, int32_t* route_pos,
                                int32_t* sorted_route, int tokens, int top_k, int hidden,
-                               hipStream_t stream);
+                               int experts, hipStream_t stream);
 hipError_t grouped_gemm_naive(const float* x, const float* w, const int32_t* offsets, float* y,
                               int experts, int hidden, int output, int max_expert_tokens,
                               hipStream_t stream);

@@ -120,23 +120,31 @@ __global__ void rr_exclusive_scan_naive_kernel(const int32_t* counts, int32_t* o
 
 // reference src/permute/cuda_naive/baseline.cu:13-34: one block per route,
 // destination = offsets[e] + atomic cursor (placement order is unspecified).
+// Routes whose id lies outside [0, experts) or whose destination lies outside
+// [0, routes) are not placed (route_pos = -1) instead of being dereferenced.
 __global__ void rr_token_permute_naive_kernel(const float* __restrict__ x,
                                               const int32_t* __restrict__ ids,
                                               const int32_t* __restrict__ offsets, int32_t* cursors,
                                               float* __restrict__ x_permuted,
                                               int32_t* __restrict__ route_pos,
                                               int32_t* __restrict__ sorted_route, int routes,
-                                              int top_k, int hidden) {
+                                              int top_k, int hidden, int experts) {
   const int route = static_cast<int>(blockIdx.x);
   if (route >= routes) return;
   __shared__ int destination;
   if (threadIdx.x == 0) {
     const int e = ids[route];
-    destination = offsets[e] + atomicAdd(cursors + e, 1);
-    route_pos[route] = destination;
-    if (sorted_route != nullptr) sorted_route[destination] = route;
+    int dest = -1;
+    if (e >= 0 && e < experts) {
+      dest = offsets[e] + atomicAdd(cursors + e, 1);
+      if (dest < 0 || dest >= routes) dest = -1;
+    }
+    destination = dest;
+    route_pos[route] = dest;
+    if (sorted_route != nullptr && dest >= 0) sorted_route[dest] = route;
   }
   __syncthreads();
+  if (destination < 0) return;
   const std::size_t token = static_cast<std::size_t>(route / top_k);
   for (int col = threadIdx.x; col < hidden; col += blockDim.x) {
     x_permuted[static_cast<std::size_t>(destination) * hidden + col] = x[token * hidden + col];
@@ -178,11 +186,14 @@ __global__ void rr_unpermute_naive_kernel(const float* __restrict__ y_permuted,
   if (linear >= tokens * output) return;
   const int token = linear / output;
   const int col = linear % output;
+  const int routes = tokens * top_k;
   float acc = 0.0F;
   for (int j = 0; j < top_k; ++j) {
     const int route = token * top_k + j;
-    const std::size_t src = static_cast<std::size_t>(route_pos[route]);
-    acc = __fadd_rn(acc, __fmul_rn(route_weights[route], y_permuted[src * output + col]));
+    const int32_t src = route_pos[route];
+    if (src < 0 || src >= routes) continue;  // never dereference an out-of-range row
+    acc = __fadd_rn(acc, __fmul_rn(route_weights[route],
+                                   y_permuted[static_cast<std::size_t>(src) * output + col]));
   }
   y[linear] = acc;
 }
@@ -229,7 +240,7 @@ hipError_t exclusive_scan_naive(const int32_t* counts, int32_t* offsets, int exp
 hipError_t token_permute_naive(const float* x, const int32_t* ids, const int32_t* offsets,
                                int32_t* cursors, float* x_permuted, int32_t* route_pos,
                                int32_t* sorted_route, int tokens, int top_k, int hidden,
-                               hipStream_t stream) {
+                               int experts, hipStream_t stream) {
   if (tokens < 0 || top_k <= 0 || hidden < 0) return hipErrorInvalidValue;
   if (tokens == 0) return hipSuccess;
   if (tokens > INT_MAX / top_k) return hipErrorInvalidValue;
@@ -240,7 +251,7 @@ hipError_t token_permute_naive(const float* x, const int32_t* ids, const int32_t
   const int routes = tokens * top_k;
   rr_token_permute_naive_kernel<<<routes, 128, 0, stream>>>(x, ids, offsets, cursors, x_permuted,
                                                             route_pos, sorted_route, routes, top_k,
-                                                            hidden);
+                                                            hidden, experts);
   return hipGetLastError();
 }
 
@@ -304,8 +315,10 @@ hipError_t rr_launch_token_permute_naive(const float* x, const int32_t* expert_i
                                          float* x_permuted, int32_t* route_pos,
                                          int32_t* sorted_route, int32_t tokens, int32_t top_k,
                                          int32_t hidden, hipStream_t stream) {
+  // The raw launcher has no expert count (reference signature); ids are trusted
+  // to index offsets, destinations are still range-checked.
   return rr::kern::token_permute_naive(x, expert_ids, offsets, cursors, x_permuted, route_pos,
-                                       sorted_route, tokens, top_k, hidden, stream);
+                                       sorted_route, tokens, top_k, hidden, INT_MAX, stream);
 }
 hipError_t rr_launch_grouped_gemm_naive(const float* x_permuted, const float* expert_weights,
                                         const int32_t* offsets, float* y_permuted,

@@ -323,7 +323,7 @@ rr_status rr_token_permute(const rr_token_permute_args* args, const rr_runtime_c
     return rr::device_status(
         rr::kern::token_permute_naive(x, args->expert_ids, args->offsets, cursors, x_permuted,
                                       args->route_pos, args->sorted_route, args->tokens,
-                                      args->top_k, args->hidden, context->stream),
+                                      args->top_k, args->hidden, args->experts, context->stream),
         "token_permute naive kernel launch failed");
   }
   if (rr::is_native(decision)) {

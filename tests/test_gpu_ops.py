@@ -339,8 +339,10 @@ def test_permute_c4_skew_full_size(ctx, device):
     xp = torch.empty(2 * tokens, hidden, device=device)
     pos = torch.empty(2 * tokens, dtype=torch.int32, device=device)
     cursors = torch.empty(experts, dtype=torch.int32, device=device)
-    args = rr.TokenPermuteArgs(x=rr.cview(p(x)), expert_ids=p(to_dev(ids.reshape(-1), device)),
-                               offsets=p(to_dev(offsets, device)), x_permuted=rr.mview(p(xp)),
+    ids_d = to_dev(ids.reshape(-1), device)  # kept alive for the call
+    offsets_d = to_dev(offsets, device)
+    args = rr.TokenPermuteArgs(x=rr.cview(p(x)), expert_ids=p(ids_d),
+                               offsets=p(offsets_d), x_permuted=rr.mview(p(xp)),
                                route_pos=p(pos), tokens=tokens, experts=experts, top_k=2, hidden=hidden)
     del x_h
     pctx = rr.RuntimeContext(stream=ctx.stream, workspace=p(cursors), workspace_bytes=experts * 4,
@@ -449,8 +451,10 @@ def run_unpermute(ctx, device, yp_h, pos_h, w_h, top_k, kernel, offset=0):
     ypb = torch.empty(yp_h.size + offset, dtype=torch.float32, device=device)
     ypb[offset:] = to_dev(yp_h.reshape(-1), device)
     yb = torch.full((tokens * output + offset,), -1.0, dtype=torch.float32, device=device)
-    args = rr.UnpermuteArgs(y_permuted=rr.cview(p(ypb) + 4 * offset), route_pos=p(to_dev(pos_h, device)),
-                            route_weights=rr.cview(p(to_dev(w_h, device))), y=rr.mview(p(yb) + 4 * offset),
+    pos_d = to_dev(pos_h, device)  # kept alive for the call
+    w_d = to_dev(w_h, device)
+    args = rr.UnpermuteArgs(y_permuted=rr.cview(p(ypb) + 4 * offset), route_pos=p(pos_d),
+                            route_weights=rr.cview(p(w_d)), y=rr.mview(p(yb) + 4 * offset),
                             tokens=tokens, top_k=top_k, output=output, kernel=kernel)
     ok(rr.unpermute(args, ctx))
     return to_host(yb)[offset:].reshape(tokens, output)
