@@ -1,0 +1,354 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 routing chain (one MI355X).
+
+Headline: chain_from_tokens at T=4096, E=64, K=256, N=128 (FP32), value =
+tokens/s over exactly --steps chains bracketed by device synchronisation.
+Every stage is also timed on its own (HIP events on the launch stream,
+average over back-to-back launches) and priced against its roofline with the
+algorithmic work model (minimum unique traffic / GEMM flops). Extras measured
+in the same run: the Mixtral-shaped grouped GEMM + permute + unpermute (C4,
+aligned and non-aligned), the fine-grained chain (C5) and the histogram-scan
+stress (C3). The CPU baseline is the reference CPU oracle chain restated in
+oracle/ (single thread), timed on the host on the same headline workload.
+
+Prints one JSON line. `--gpus N` with N > 1 exits with a message: this build
+runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, vendor peak
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor peak
+RIDGE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # flop/byte
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--stage-reps", type=int, default=100)
+    ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    ap.add_argument("--only", default="", help="comma list of extras to run: c3,c4,c4u,c5")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------ work model
+
+def work_model(t, e, k, n, active=None, sorted_route=False):
+    """Algorithmic bytes / flops per stage (FP32 = 4 bytes, R = 2T)."""
+    r = 2 * t
+    active = e if active is None else active
+    return {
+        "dense_gemm": (4 * (t * k + k * e + t * e), 2.0 * t * k * e),
+        "topk_gate": (4 * t * e + 8 * r, 0.0),
+        "histogram_scan": (4 * r + 4 * e + 4 * (e + 1), 0.0),
+        "token_permute": (4 * t * k + 4 * r * k + 4 * r + 4 * (e + 1) + 4 * r + (4 * r if sorted_route else 0), 0.0),
+        "grouped_gemm": (4 * (r * k + active * k * n + r * n) + 4 * (e + 1), 2.0 * r * k * n),
+        "unpermute": (4 * r * n + 4 * t * n + 8 * r, 3.0 * t * n),
+    }
+
+
+def roofline(name, nbytes, flops, seconds):
+    ai = flops / nbytes if nbytes else 0.0
+    if flops and ai > RIDGE:
+        achieved = flops / seconds / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4)}
+    achieved = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4)}
+
+
+# ------------------------------------------------------------------- harness
+
+class Chain:
+    """Device buffers + per-stage argument structs of one chain workload."""
+
+    def __init__(self, cfg, inputs, device, with_inverse=False):
+        import torch
+        import raggedroute_amd as rr
+        self.rr, self.torch, self.cfg = rr, torch, cfg
+        t, e, k, n = cfg.tokens, cfg.experts, cfg.hidden, cfg.output
+        i32 = dict(dtype=torch.int32, device=device)
+        self.x, self.we = inputs["x"], inputs["expert_weights"]
+        self.wr = inputs.get("router_weights")
+        self.logits = inputs["logits"] if "logits" in inputs else torch.empty(t, e, device=device)
+        self.ids = torch.empty(t, 2, **i32)
+        self.w = torch.empty(t, 2, device=device)
+        self.counts = torch.empty(e, **i32)
+        self.offsets = torch.empty(e + 1, **i32)
+        self.xp = torch.empty(2 * t, k, device=device)
+        self.pos = torch.empty(2 * t, **i32)
+        self.inv = torch.empty(2 * t, **i32) if with_inverse else None
+        self.yp = torch.empty(2 * t, n, device=device)
+        self.y = torch.empty(t, n, device=device)
+        self.cursors = torch.empty(e, **i32)
+        ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+        self.stream = torch.cuda.current_stream(device).cuda_stream
+        self.ctx = rr.RuntimeContext(stream=self.stream, workspace=self.cursors.data_ptr(),
+                                     workspace_bytes=e * 4, architecture=int(rr.DeviceArchitecture.kGfx950))
+        self.chain_args = rr.ChainArgs(
+            x=ptr(self.x), router_weights=ptr(self.wr), logits=ptr(self.logits), expert_ids=ptr(self.ids),
+            route_weights=ptr(self.w), counts=ptr(self.counts), offsets=ptr(self.offsets),
+            x_permuted=ptr(self.xp), route_pos=ptr(self.pos), sorted_route=ptr(self.inv),
+            expert_weights=ptr(self.we), y_permuted=ptr(self.yp), y=ptr(self.y),
+            tokens=t, experts=e, hidden=k, output=n)
+        cv, mv = rr.cview, rr.mview
+        self.stage_args = {
+            "dense_gemm": (rr.dense_gemm, rr.DenseGemmArgs(a=cv(ptr(self.x)), b=cv(ptr(self.wr)),
+                                                           c=mv(ptr(self.logits)), m=t, n=e, k=k)),
+            "topk_gate": (rr.topk_gate, rr.TopKGateArgs(logits=cv(ptr(self.logits)), expert_ids=ptr(self.ids),
+                                                        weights=mv(ptr(self.w)), tokens=t, experts=e)),
+            "histogram_scan": (rr.histogram_exclusive_scan, rr.HistogramExclusiveScanArgs(
+                expert_ids=ptr(self.ids), counts=ptr(self.counts), offsets=ptr(self.offsets),
+                route_pairs=2 * t, experts=e)),
+            "token_permute": (rr.token_permute, rr.TokenPermuteArgs(
+                x=cv(ptr(self.x)), expert_ids=ptr(self.ids), offsets=ptr(self.offsets), x_permuted=mv(ptr(self.xp)),
+                route_pos=ptr(self.pos), sorted_route=ptr(self.inv), tokens=t, experts=e, top_k=2, hidden=k)),
+            "grouped_gemm": (rr.grouped_gemm, rr.GroupedGemmArgs(
+                x_permuted=cv(ptr(self.xp)), expert_weights=cv(ptr(self.we)), offsets=ptr(self.offsets),
+                y_permuted=mv(ptr(self.yp)), experts=e, hidden=k, output=n, max_expert_tokens=2 * t)),
+            "unpermute": (rr.unpermute, rr.UnpermuteArgs(
+                y_permuted=cv(ptr(self.yp)), route_pos=ptr(self.pos), route_weights=cv(ptr(self.w)),
+                y=mv(ptr(self.y)), tokens=t, top_k=2, output=n)),
+        }
+        if not cfg.from_tokens:
+            del self.stage_args["dense_gemm"]
+
+    def chain(self):
+        fn = self.rr.chain_from_tokens if self.cfg.from_tokens else self.rr.chain_from_logits
+        status = fn(self.chain_args, self.ctx)
+        if not status.ok():
+            raise RuntimeError(status.message)
+
+    def stage(self, name):
+        fn, args = self.stage_args[name]
+        status = fn(args, self.ctx)
+        if not status.ok():
+            raise RuntimeError(f"{name}: {status.message}")
+
+
+def time_loop(torch, fn, reps, warmup=3):
+    """Average seconds per call of `fn` over `reps` back-to-back launches,
+    bracketed by HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / reps
+
+
+def stage_report(torch, ch, reps, model):
+    out = {}
+    for name in ch.stage_args:
+        sec = time_loop(torch, lambda: ch.stage(name), reps)
+        nbytes, flops = model[name]
+        out[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "flops": flops,
+                     "roofline": roofline(name, nbytes, flops, sec)}
+    return out
+
+
+# ------------------------------------------------------------------ workloads
+
+def headline(torch, device, args):
+    from raggedroute_amd import workloads
+    cfg = workloads.HEADLINE
+    inputs = workloads.chain_inputs_device(cfg, 0, device)
+    ch = Chain(cfg, inputs, device)
+    for _ in range(args.warmup):
+        ch.chain()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        ch.chain()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    elapsed = start.elapsed_time(stop) / 1e3
+    # per-chain p50 over single-chain event spans (reference runner p50 semantics)
+    spans = []
+    for _ in range(min(args.steps, 100)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(); ch.chain(); b.record()
+        b.synchronize()
+        spans.append(a.elapsed_time(b) / 1e3)
+    active = int((ch.counts.cpu().numpy() > 0).sum())
+    model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
+    stages = stage_report(torch, ch, args.stage_reps, model)
+    return cfg, ch, inputs, {"elapsed_s": elapsed, "wall_s": wall, "p50_s": statistics.median(spans),
+                             "stages": stages, "active_experts": active}
+
+
+def c4(torch, device, hidden=4096, output=14336, reps=5):
+    """Mixtral-shaped ragged grouped GEMM + permute + unpermute: T=8192, R=16384,
+    E=8 with 7 active (Zipf 1.2), expert 7 empty."""
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    t, e = 8192, 8
+    ids_h, w_h = workloads.c4_routing(t, e, 7, 1.2, seed=0)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    x = torch.empty(t, hidden, device=device)
+    we = torch.empty(e, hidden, output, device=device)
+    assert rr.fill_normal(x.data_ptr(), x.numel(), 0, workloads.S_X, 0.0, 1.0, stream) == 0
+    sd = float(np.float32(1.0 / np.sqrt(hidden)))
+    assert rr.fill_normal(we.data_ptr(), we.numel(), 0, workloads.S_EXPERTS, 0.0, sd, stream) == 0
+    cfg = workloads.ChainConfig("C4", t, e, hidden, output, from_tokens=False)
+    ch = Chain(cfg, {"x": x, "expert_weights": we, "logits": torch.empty(t, e, device=device)}, device)
+    ch.ids.copy_(torch.from_numpy(ids_h))
+    ch.w.copy_(torch.from_numpy(w_h))
+    for name in ("histogram_scan", "token_permute", "grouped_gemm", "unpermute"):
+        ch.stage(name)
+    torch.cuda.synchronize()
+    active = int((ch.counts.cpu().numpy() > 0).sum())
+    model = work_model(t, e, hidden, output, active)
+    out = {"T": t, "E": e, "K": hidden, "N": output, "active_experts": active}
+    for name, n_reps in (("token_permute", 50), ("grouped_gemm", reps), ("unpermute", 50)):
+        sec = time_loop(torch, lambda: ch.stage(name), n_reps, warmup=1)
+        nbytes, flops = model[name]
+        out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
+    out["permute_gbs_reference_model"] = round(2 * 4 * 2 * t * hidden / (out["token_permute"]["us"] * 1e-6) / 1e9, 1)
+    del ch, x, we
+    torch.cuda.empty_cache()
+    return out
+
+
+def c5(torch, device, steps=20):
+    from raggedroute_amd import workloads
+    cfg = workloads.C5
+    inputs = workloads.chain_inputs_device(cfg, 0, device)
+    ch = Chain(cfg, inputs, device)
+    sec = time_loop(torch, ch.chain, steps, warmup=3)
+    active = int((ch.counts.cpu().numpy() > 0).sum())
+    model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
+    stages = stage_report(torch, ch, 10, model)
+    del ch, inputs
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1), "stages": stages}
+
+
+def c3(torch, device):
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    routes = 1 << 20
+    out = {}
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ctx = rr.RuntimeContext(stream=stream, architecture=int(rr.DeviceArchitecture.kGfx950))
+    for experts in (1, 33, 256):
+        for dist in ("uniform", "hot50"):
+            ids = torch.from_numpy(workloads.route_ids(routes, experts, dist, 0)).to(device)
+            counts = torch.empty(experts, dtype=torch.int32, device=device)
+            offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
+            args = rr.HistogramExclusiveScanArgs(expert_ids=ids.data_ptr(), counts=counts.data_ptr(),
+                                                 offsets=offsets.data_ptr(), route_pairs=routes, experts=experts)
+            sec = time_loop(torch, lambda: rr.histogram_exclusive_scan(args, ctx), 50)
+            nbytes = 4 * routes + 4 * experts + 4 * (experts + 1)
+            out[f"E{experts}_{dist}"] = {"us": round(sec * 1e6, 2),
+                                        "gbs": round(nbytes / sec / 1e9, 1)}
+    return out
+
+
+def cpu_baseline(inputs_host, budget_s):
+    """Reference CPU oracle chain (oracle/, single thread, -O2
+    -ffp-contract=off) on the full headline workload, median over repeats."""
+    import oracle
+    runs = []
+    t_start = time.perf_counter()
+    while len(runs) < 25 and (len(runs) < 3 or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        oracle.chain(inputs_host["x"], inputs_host["expert_weights"], router_weights=inputs_host["router_weights"])
+        runs.append(time.perf_counter() - t0)
+    return statistics.median(runs), len(runs)
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one MI355X; "
+                                   "multi-GPU runs are not part of it (each GPU would run the same "
+                                   "chain on its own token shard)"}))
+        return 2
+    import torch
+    import raggedroute_amd  # noqa: F401  (loads the HIP library or fails)
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    cfg, ch, inputs, head = headline(torch, device, args)
+    tokens_per_s = cfg.tokens * args.steps / head["elapsed_s"]
+    stages = head["stages"]
+    dominant = max(stages, key=lambda s: stages[s]["us"])
+    roof = dict(stages[dominant]["roofline"])
+    roof["kernel"] = dominant
+    roof["traffic"] = None
+    traffic_file = REPO / "profiles" / f"{dominant}_headline_traffic.json"
+    if traffic_file.exists():
+        roof["traffic"] = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+
+    extras = {}
+    if not args.quick:
+        only = set(filter(None, args.only.split(","))) or {"c3", "c4", "c4u", "c5"}
+        if "c4" in only:
+            extras["C4"] = c4(torch, device)
+        if "c4u" in only:
+            extras["C4_nonaligned"] = c4(torch, device, 4095, 14335, reps=3)
+        if "c5" in only:
+            extras["C5"] = c5(torch, device)
+        if "c3" in only:
+            extras["C3"] = c3(torch, device)
+
+    cpu = None
+    if not args.quick:
+        host = {k: v.cpu().numpy() for k, v in inputs.items()}
+        sec, runs = cpu_baseline(host, args.cpu_seconds)
+        cpu = {"value": round(cfg.tokens / sec, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"full headline chain_from_tokens (T={cfg.tokens}, E={cfg.experts}, K={cfg.hidden}, "
+                         f"N={cfg.output}) on the oracle/ C restatement of the reference CPU chain, "
+                         f"median of {runs} runs", "host_cpus": os.cpu_count()}
+
+    line = {
+        "metric": "chain_from_tokens tokens/s @T4096/E64 FP32; grouped GEMM TFLOP/s; GB/s",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["elapsed_s"] / args.steps * 1e3, 4),
+        "p50_chain_us": round(head["p50_s"] * 1e6, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (SplitMix64 normal inputs generated in HBM, seed 0)",
+        "config": {"workload": "chain_from_tokens", "T": cfg.tokens, "E": cfg.experts, "K": cfg.hidden,
+                   "N": cfg.output, "top_k": 2, "active_experts": head["active_experts"]},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "stages": stages,
+        "extras": extras,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

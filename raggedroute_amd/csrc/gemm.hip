@@ -134,7 +134,9 @@ __device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles,
   *ct = within / rows_in_group;
 }
 
-template <class S, bool VEC>
+// GROUPED = false: one dense segment of dense_rows rows with weights W (the
+// router GEMM); true: ragged segments from offsets with weights W[e].
+template <class S, bool VEC, bool GROUPED>
 __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
     const float* __restrict__ X, const float* __restrict__ W, const int32_t* __restrict__ offsets,
     float* __restrict__ Y, int experts, int dense_rows, int K, int N) {
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
 
   // ---- device-side scheduler: per-expert row-tile prefix in LDS ----
   for (int e = tid; e <= experts; e += S::kThreads) {
-    s_off[e] = offsets != nullptr ? offsets[e] : (e == 0 ? 0 : dense_rows);
+    s_off[e] = GROUPED ? offsets[e] : (e == 0 ? 0 : dense_rows);
   }
   __syncthreads();
   if (wave == 0) {
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
     const int row0 = s_off[e] + (rt - s_pre[e]) * S::BM;
     const int row_end = s_off[e + 1];
     const int n0 = ct * S::BN;
-    const float* B = W + static_cast<std::size_t>(offsets != nullptr ? e : 0) * K * N;
+    const float* B = W + static_cast<std::size_t>(GROUPED ? e : 0) * K * N;
 
     v4f acc[S::kTM][S::kTN];
 #pragma unroll
@@ -299,12 +301,21 @@ hipError_t launch_gemm(const float* x, const float* w, const int32_t* offsets, f
   if (grid < 1) grid = 1;
   const std::size_t lds = 2 * S::kStageFloats * sizeof(float) +
                           2 * static_cast<std::size_t>(experts + 1) * sizeof(int32_t);
-  if (vec) {
-    rr_gemm_mfma_kernel<S, true><<<static_cast<unsigned>(grid), S::kThreads, lds, stream>>>(
-        x, w, offsets, y, experts, dense_rows, K, N);
+  const dim3 g(static_cast<unsigned>(grid));
+  if (offsets != nullptr) {
+    if (vec) {
+      rr_gemm_mfma_kernel<S, true, true><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
+                                                                          dense_rows, K, N);
+    } else {
+      rr_gemm_mfma_kernel<S, false, true><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
+                                                                           dense_rows, K, N);
+    }
+  } else if (vec) {
+    rr_gemm_mfma_kernel<S, true, false><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
+                                                                         dense_rows, K, N);
   } else {
-    rr_gemm_mfma_kernel<S, false><<<static_cast<unsigned>(grid), S::kThreads, lds, stream>>>(
-        x, w, offsets, y, experts, dense_rows, K, N);
+    rr_gemm_mfma_kernel<S, false, false><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
+                                                                          dense_rows, K, N);
   }
   return hipGetLastError();
 }
