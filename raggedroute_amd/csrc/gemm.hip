@@ -6,10 +6,12 @@
 // LDS, builds the per-expert row-tile prefix and walks the tile space
 // (row tiles of every expert x column tiles) with a grid-stride loop.
 //
-// Tile: BM x BN per workgroup, BK = 16 per LDS stage, two LDS stages plus a
-// register prefetch of the next stage. LDS holds both operands k-contiguous
-// ([m][k] and [n][k], rows padded to 20 floats) so every MFMA operand fetch is
-// one ds_read_b128 covering four consecutive MFMA k-steps. Lane l (group
+// Tile: BM x BN per workgroup, BK per LDS stage (16 for the large tile, 64 for
+// the small-K tiles so a K = 256 problem takes four pipeline steps instead of
+// sixteen dependent global round trips), two LDS stages plus a register
+// prefetch of the next stage. LDS holds both operands k-contiguous ([m][k] and
+// [n][k], rows padded by 4 floats) so every MFMA operand fetch is one
+// ds_read_b128 covering four consecutive MFMA k-steps. Lane l (group
 // g = l / 16, index i = l % 16) supplies A[m0 + i][k] and B[k][n0 + i] for
 // k = kk + 4g + s at MFMA step s, which is the same k for both operands.
 #include <hip/hip_runtime.h>
@@ -18,6 +20,8 @@
 #include <climits>
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 
 #include "launchers.h"
 #include "raggedroute_capi.h"
@@ -28,25 +32,30 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 16;
-constexpr int kLd = kBK + 4;  // padded LDS row (floats)
 constexpr int kGroupM = 8;    // row tiles per swizzle group
 constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dispatched round-robin
 
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int WM_, int WN_, int BK_>
 struct TileShape {
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int WM = WM_;
   static constexpr int WN = WN_;
+  static constexpr int BK = BK_;
+  static constexpr int kLd = BK + 4;  // padded LDS row (floats)
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int kTM = BM / WM / 16;  // 16x16 MFMA tiles per wave along M
   static constexpr int kTN = BN / WN / 16;
-  static constexpr int kALoads = BM * kBK / 4 / kThreads;  // float4 slots per thread
-  static constexpr int kBLoads = BN * kBK / 4 / kThreads;
+  static constexpr int kALoads = BM * BK / 4 / kThreads;  // float4 slots per thread
+  static constexpr int kBLoads = BN * BK / 4 / kThreads;
   static constexpr int kStageFloats = (BM + BN) * kLd;
+  // BK >= 128 tiles stage the whole K extent of a short-K problem at once: one
+  // global round trip and one barrier per tile, a single LDS stage.
+  static constexpr int kStages = BK >= 128 ? 1 : 2;
+  static_assert(BK % 16 == 0 && (BK & (BK - 1)) == 0, "BK is a power of two >= 16");
+  static_assert(kTM >= 1 && kTN >= 1, "wave tile below one MFMA tile");
   static_assert(kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
-  static_assert(BM * kBK / 4 % kThreads == 0 && BN * kBK / 4 % kThreads == 0, "uneven loads");
+  static_assert(BM * BK / 4 % kThreads == 0 && BN * BK / 4 % kThreads == 0, "uneven loads");
 };
 
 // Global -> register staging of one BK slice. A rows are k-contiguous in
@@ -62,8 +71,8 @@ struct Stage {
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int r = f >> 2;            // BK / 4 = 4 float4 per row
-      const int c = (f & 3) * 4;
+      const int r = f / (S::BK / 4);   // BK / 4 float4 per row
+      const int c = (f % (S::BK / 4)) * 4;
       const int row = row0 + r;
       const int k = k0 + c;
       const float* src = A + static_cast<std::size_t>(row) * K + k;
@@ -82,8 +91,8 @@ struct Stage {
 #pragma unroll
     for (int p = 0; p < S::kBLoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int kr = f & (kBK - 1);  // k varies fastest across lanes
-      const int n = (f >> 4) * 4;
+      const int kr = f & (S::BK - 1);  // k varies fastest across lanes
+      const int n = (f / S::BK) * 4;
       const int k = k0 + kr;
       const int col = n0 + n;
       const float* src = B + static_cast<std::size_t>(k) * N + col;
@@ -103,21 +112,22 @@ struct Stage {
 
   __device__ __forceinline__ void store(float* __restrict__ lds, int tid) const {
     float* As = lds;
-    float* Bs = lds + S::BM * kLd;
+    float* Bs = lds + S::BM * S::kLd;
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int r = f >> 2;
-      const int c = (f & 3) * 4;
-      *reinterpret_cast<float4*>(As + r * kLd + c) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
+      const int r = f / (S::BK / 4);
+      const int c = (f % (S::BK / 4)) * 4;
+      *reinterpret_cast<float4*>(As + r * S::kLd + c) =
+          make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
     }
 #pragma unroll
     for (int p = 0; p < S::kBLoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int kr = f & (kBK - 1);
-      const int n = (f >> 4) * 4;
+      const int kr = f & (S::BK - 1);
+      const int n = (f / S::BK) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) Bs[(n + j) * kLd + kr] = b[p][j];
+      for (int j = 0; j < 4; ++j) Bs[(n + j) * S::kLd + kr] = b[p][j];
     }
   }
 };
@@ -141,8 +151,8 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
     const float* __restrict__ X, const float* __restrict__ W, const int32_t* __restrict__ offsets,
     float* __restrict__ Y, int experts, int dense_rows, int K, int N) {
   extern __shared__ float lds[];
-  float* stages = lds;                                              // 2 stages
-  int32_t* s_off = reinterpret_cast<int32_t*>(lds + 2 * S::kStageFloats);  // [experts + 1]
+  float* stages = lds;                                                       // kStages stages
+  int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * S::kStageFloats);  // [experts + 1]
   int32_t* s_pre = s_off + experts + 1;                             // [experts + 1]
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = rr::dev::lane_id();
@@ -191,7 +201,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
   const int wn0 = (wave % S::WN) * (S::BN / S::WN);
   const int g = lane >> 4;
   const int li = lane & 15;
-  const int nk = (K + kBK - 1) / kBK;
+  const int nk = (K + S::BK - 1) / S::BK;
 
   for (long t = worker; t < total; t += grid) {
     int rt, ct;
@@ -221,20 +231,20 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
     }
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
-      const float* cur = stages + (kt & 1) * S::kStageFloats;
-      if (kt + 1 < nk) st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * kBK, tid);
+      const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
+      if (S::kStages > 1 && kt + 1 < nk) st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
       const float* As = cur;
-      const float* Bs = cur + S::BM * kLd;
+      const float* Bs = cur + S::BM * S::kLd;
 #pragma unroll
-      for (int kk = 0; kk < kBK; kk += 16) {
+      for (int kk = 0; kk < S::BK; kk += 16) {
         float4 af[S::kTM], bf[S::kTN];
 #pragma unroll
         for (int i = 0; i < S::kTM; ++i) {
-          af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * kLd + kk + 4 * g);
+          af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * S::kLd + kk + 4 * g);
         }
 #pragma unroll
         for (int j = 0; j < S::kTN; ++j) {
-          bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * kLd + kk + 4 * g);
+          bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * S::kLd + kk + 4 * g);
         }
 #pragma unroll
         for (int i = 0; i < S::kTM; ++i) {
@@ -247,7 +257,13 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
           }
         }
       }
-      if (kt + 1 < nk) st.store(stages + ((kt + 1) & 1) * S::kStageFloats, tid);
+      if (S::kStages > 1 && kt + 1 < nk) {
+        st.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
+      } else if (S::kStages == 1 && kt + 1 < nk) {
+        __syncthreads();  // every wave is done with the single stage
+        st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+        st.store(stages, tid);
+      }
       __syncthreads();
     }
 
@@ -290,6 +306,26 @@ int device_cu_count() {
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
+// Allows a kernel instantiation to use the whole 160 KB of gfx950 LDS as
+// dynamic shared memory (once per instantiation).
+template <class Kernel>
+hipError_t allow_full_lds(Kernel kernel) {
+  static const hipError_t status = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return status;
+}
+
+template <class S, bool VEC, bool GROUPED>
+hipError_t launch_one(dim3 grid, std::size_t lds, const float* x, const float* w,
+                      const int32_t* offsets, float* y, int experts, int dense_rows, int K, int N,
+                      hipStream_t stream) {
+  const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, GROUPED>);
+  if (attr != hipSuccess) return attr;
+  rr_gemm_mfma_kernel<S, VEC, GROUPED><<<grid, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
+                                                                           dense_rows, K, N);
+  return hipGetLastError();
+}
+
 template <class S>
 hipError_t launch_gemm(const float* x, const float* w, const int32_t* offsets, float* y,
                        int experts, int dense_rows, int K, int N, long tile_bound,
@@ -299,29 +335,49 @@ hipError_t launch_gemm(const float* x, const float* w, const int32_t* offsets, f
   long grid = tile_bound < cap ? tile_bound : cap;
   if (grid >= kXcds) grid = grid / kXcds * kXcds;
   if (grid < 1) grid = 1;
-  const std::size_t lds = 2 * S::kStageFloats * sizeof(float) +
+  const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) +
                           2 * static_cast<std::size_t>(experts + 1) * sizeof(int32_t);
   const dim3 g(static_cast<unsigned>(grid));
   if (offsets != nullptr) {
-    if (vec) {
-      rr_gemm_mfma_kernel<S, true, true><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
-                                                                          dense_rows, K, N);
-    } else {
-      rr_gemm_mfma_kernel<S, false, true><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
-                                                                           dense_rows, K, N);
-    }
-  } else if (vec) {
-    rr_gemm_mfma_kernel<S, true, false><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
-                                                                         dense_rows, K, N);
-  } else {
-    rr_gemm_mfma_kernel<S, false, false><<<g, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
-                                                                          dense_rows, K, N);
+    return vec ? launch_one<S, true, true>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream)
+               : launch_one<S, false, true>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream);
   }
-  return hipGetLastError();
+  return vec ? launch_one<S, true, false>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream)
+             : launch_one<S, false, false>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream);
 }
 
-using TileLarge = TileShape<128, 128, 2, 2>;  // 4 waves, 64x64 per wave
-using TileSmall = TileShape<64, 64, 2, 2>;    // 4 waves, 32x32 per wave
+// 128x128, four 64x64 waves, BK 16: large problems (C4, C5 grouped).
+using TileLarge = TileShape<128, 128, 2, 2, 16>;
+// 64x64, four 32x32 waves, BK 64: medium problems with short K loops.
+using TileSmall = TileShape<64, 64, 2, 2, 64>;
+// 32x64, four 16x32 waves, BK 64: small ragged segments (tens of rows per expert).
+using TileMedium = TileShape<32, 64, 2, 2, 64>;
+// 16x64, four 16x16 waves side by side, BK 64: narrow router GEMMs (N = E).
+using TileNarrow = TileShape<16, 64, 1, 4, 64>;
+
+// Whole-K tiles (K <= 256): one LDS stage holds all of K.
+using TileSmallK256 = TileShape<64, 64, 2, 2, 256>;    // 133 KB LDS
+using TileMediumK256 = TileShape<32, 64, 2, 2, 256>;   // 100 KB LDS
+using TileNarrowK256 = TileShape<16, 64, 1, 4, 256>;   // 83 KB LDS
+
+// Tile override for tuning sweeps: RR_GEMM_TILE = large | small | medium |
+// narrow | small256 | medium256 | narrow256 forces one of the (equally
+// correct) tile configurations.
+int tile_override() {
+  static const int choice = [] {
+    const char* v = std::getenv("RR_GEMM_TILE");
+    if (v == nullptr) return 0;
+    if (std::strcmp(v, "large") == 0) return 1;
+    if (std::strcmp(v, "small") == 0) return 2;
+    if (std::strcmp(v, "medium") == 0) return 3;
+    if (std::strcmp(v, "narrow") == 0) return 4;
+    if (std::strcmp(v, "small256") == 0) return 5;
+    if (std::strcmp(v, "medium256") == 0) return 6;
+    if (std::strcmp(v, "narrow256") == 0) return 7;
+    return 0;
+  }();
+  return choice;
+}
 
 long ceil_div(long a, long b) { return (a + b - 1) / b; }
 
@@ -330,24 +386,56 @@ long tile_bound(int experts, long rows_per_expert, int bm, int n, int bn) {
   return static_cast<long>(experts) * ceil_div(rows_per_expert, bm) * ceil_div(n, bn);
 }
 
+// Expected tile count: full tiles of the rows plus one partial tile per segment.
+long tile_estimate(long rows, int segments, int bm, int n, int bn) {
+  return (ceil_div(rows, bm) + segments) * ceil_div(n, bn);
+}
+
 hipError_t gemm_dispatch(const float* x, const float* w, const int32_t* offsets, float* y,
                          int experts, int dense_rows, int K, int N, long rows_per_expert,
                          long total_rows_estimate, hipStream_t stream) {
   const long cus = device_cu_count();
-  // Prefer the 128x128 tile when it still yields two tiles per CU.
-  const long large_tiles =
-      (ceil_div(total_rows_estimate, TileLarge::BM) + (offsets ? experts : 0)) *
-      ceil_div(N, TileLarge::BN);
-  if (large_tiles >= 2 * cus) {
-    return launch_gemm<TileLarge>(x, w, offsets, y, experts, dense_rows, K, N,
-                                  tile_bound(experts, rows_per_expert, TileLarge::BM, N,
-                                             TileLarge::BN),
-                                  stream);
+  const int segments = offsets != nullptr ? experts : 0;
+  switch (tile_override()) {
+    case 1:
+      return launch_gemm<TileLarge>(x, w, offsets, y, experts, dense_rows, K, N,
+                                    tile_bound(experts, rows_per_expert, TileLarge::BM, N, TileLarge::BN), stream);
+    case 2:
+      return launch_gemm<TileSmall>(x, w, offsets, y, experts, dense_rows, K, N,
+                                    tile_bound(experts, rows_per_expert, TileSmall::BM, N, TileSmall::BN), stream);
+    case 3:
+      return launch_gemm<TileMedium>(x, w, offsets, y, experts, dense_rows, K, N,
+                                     tile_bound(experts, rows_per_expert, TileMedium::BM, N, TileMedium::BN), stream);
+    case 4:
+      return launch_gemm<TileNarrow>(x, w, offsets, y, experts, dense_rows, K, N,
+                                     tile_bound(experts, rows_per_expert, TileNarrow::BM, N, TileNarrow::BN), stream);
+    case 5:
+      return launch_gemm<TileSmallK256>(x, w, offsets, y, experts, dense_rows, K, N,
+                                        tile_bound(experts, rows_per_expert, 64, N, 64), stream);
+    case 6:
+      return launch_gemm<TileMediumK256>(x, w, offsets, y, experts, dense_rows, K, N,
+                                         tile_bound(experts, rows_per_expert, 32, N, 64), stream);
+    case 7:
+      return launch_gemm<TileNarrowK256>(x, w, offsets, y, experts, dense_rows, K, N,
+                                         tile_bound(experts, rows_per_expert, 16, N, 64), stream);
+    default:
+      break;
   }
-  return launch_gemm<TileSmall>(x, w, offsets, y, experts, dense_rows, K, N,
-                                tile_bound(experts, rows_per_expert, TileSmall::BM, N,
-                                           TileSmall::BN),
-                                stream);
+  // Largest tile that still gives every CU work (two tiles per CU for the
+  // large tile, whose LDS and registers allow two resident workgroups).
+  if (tile_estimate(total_rows_estimate, segments, TileLarge::BM, N, TileLarge::BN) >= 2 * cus) {
+    return launch_gemm<TileLarge>(
+        x, w, offsets, y, experts, dense_rows, K, N,
+        tile_bound(experts, rows_per_expert, TileLarge::BM, N, TileLarge::BN), stream);
+  }
+  if (tile_estimate(total_rows_estimate, segments, TileSmall::BM, N, TileSmall::BN) >= cus) {
+    return launch_gemm<TileSmall>(
+        x, w, offsets, y, experts, dense_rows, K, N,
+        tile_bound(experts, rows_per_expert, TileSmall::BM, N, TileSmall::BN), stream);
+  }
+  return launch_gemm<TileNarrow>(
+      x, w, offsets, y, experts, dense_rows, K, N,
+      tile_bound(experts, rows_per_expert, TileNarrow::BM, N, TileNarrow::BN), stream);
 }
 
 }  // namespace
