@@ -96,11 +96,16 @@ class Chain:
         self.inv = torch.empty(2 * t, **i32) if with_inverse else None
         self.yp = torch.empty(2 * t, n, device=device)
         self.y = torch.empty(t, n, device=device)
-        self.cursors = torch.empty(e, **i32)
         ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
         self.stream = torch.cuda.current_stream(device).cuda_stream
-        self.ctx = rr.RuntimeContext(stream=self.stream, workspace=self.cursors.data_ptr(),
-                                     workspace_bytes=e * 4, architecture=int(rr.DeviceArchitecture.kGfx950))
+        # chain workspace: E cursor words (also the token_permute workspace)
+        # followed by the fused path's sorted_route scratch
+        ws_words = rr.get_chain_workspace_size(rr.ChainArgs(tokens=t, experts=e)) // 4
+        self.workspace = torch.empty(ws_words, **i32)
+        self.cursors = self.workspace[:e]
+        self.ctx = rr.RuntimeContext(stream=self.stream, workspace=self.workspace.data_ptr(),
+                                     workspace_bytes=ws_words * 4,
+                                     architecture=int(rr.DeviceArchitecture.kGfx950))
         self.chain_args = rr.ChainArgs(
             x=ptr(self.x), router_weights=ptr(self.wr), logits=ptr(self.logits), expert_ids=ptr(self.ids),
             route_weights=ptr(self.w), counts=ptr(self.counts), offsets=ptr(self.offsets),

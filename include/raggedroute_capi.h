@@ -273,7 +273,8 @@ size_t rr_histogram_exclusive_scan_workspace_size(const rr_histogram_exclusive_s
 size_t rr_token_permute_workspace_size(const rr_token_permute_args* args);
 size_t rr_grouped_gemm_workspace_size(const rr_grouped_gemm_args* args);
 size_t rr_unpermute_workspace_size(const rr_unpermute_args* args);
-/* no reference counterpart (chain entries are new); cursor words for the permute stage */
+/* no reference counterpart (chain entries are new): (experts + 2 * tokens)
+ * int32 words = permute cursors + sorted_route scratch for the fused path */
 size_t rr_chain_workspace_size(const rr_chain_args* args);
 
 /* reference include/raggedroute/operators.h:127 / src/dense_gemm/operator.cpp:18-58 */

@@ -2,15 +2,24 @@
 //
 // The stage order is the one of reference benchmarks/adapters/chain_adapter.cpp:263-467:
 // dense GEMM -> top-2 gate -> histogram+scan -> token permute -> grouped GEMM
-// -> unpermute, all on the caller's stream, with no host synchronisation; the
-// grouped GEMM gets the worst-case launch bound max_expert_tokens = R
-// (reference chain_adapter.cpp:391-401). Each stage goes through the public C
-// ABI entry, so stage validation is identical to calling the operators one by one.
+// -> unpermute, all on the caller's stream, with no host synchronisation.
+//
+// Auto / optimized family: three fused launches that write every output of the
+// seven stages with the same values as running them one by one:
+//   1. router GEMM with the top-2 gate in its epilogue (gate kernel for
+//      chain_from_logits), also zeroing y;
+//   2. route preparation: counts, offsets, stable route_pos, sorted_route, cursors;
+//   3. grouped GEMM gathering x rows through sorted_route, writing x_permuted
+//      and y_permuted and adding both weighted routes of each token into y.
+// Naive family: the seven stages through the public C ABI entries (the grouped
+// GEMM gets the worst-case launch bound max_expert_tokens = R, reference
+// chain_adapter.cpp:391-401).
 #include <climits>
 #include <cstddef>
 #include <cstdint>
 
 #include "common.h"
+#include "launchers.h"
 
 namespace rr {
 namespace {
@@ -41,12 +50,43 @@ rr_status validate_chain(const rr_chain_args* a, const rr_runtime_context* conte
                          (from_tokens && a->router_weights == nullptr))) {
     return invalid_argument("chain received a null device pointer");
   }
-  const size_t cursor_bytes = static_cast<size_t>(a->experts) * sizeof(int32_t);
-  if (context->workspace == nullptr || context->workspace_bytes < cursor_bytes) {
+  if (context->workspace == nullptr || context->workspace_bytes < rr_chain_workspace_size(a)) {
     return make_status(RR_STATUS_INSUFFICIENT_WORKSPACE,
-                       "chain requires int32 cursor workspace for every expert");
+                       "chain requires rr_chain_workspace_size bytes of int32 workspace");
+  }
+  if (!is_aligned(context->workspace, alignof(int32_t))) {
+    return invalid_argument("chain workspace is not int32 aligned");
   }
   return ok_status();
+}
+
+// Fused path (auto / optimized family); see the file comment.
+rr_status run_fused(const rr_chain_args* a, const rr_runtime_context& ctx, bool from_tokens) noexcept {
+  auto* cursors = static_cast<int32_t*>(ctx.workspace);
+  int32_t* sorted_route = a->sorted_route != nullptr ? a->sorted_route : cursors + a->experts;
+  const int routes = a->tokens * 2;
+  hipError_t err = hipSuccess;
+  if (from_tokens && a->experts <= 128) {
+    err = kern::router_gate_mfma(a->x, a->router_weights, a->logits, a->expert_ids,
+                                 a->route_weights, a->y, a->output, a->tokens, a->experts,
+                                 a->hidden, ctx.stream);
+  } else {
+    if (from_tokens) {
+      err = kern::dense_gemm_mfma(a->x, a->router_weights, a->logits, a->tokens, a->experts,
+                                  a->hidden, ctx.stream);
+      if (err != hipSuccess) return device_status(err, "chain router GEMM launch failed");
+    }
+    err = kern::topk_gate_wave(a->logits, a->expert_ids, a->route_weights, a->tokens, a->experts,
+                               ctx.stream, a->y, a->output);
+  }
+  if (err != hipSuccess) return device_status(err, "chain gate launch failed");
+  err = kern::route_prep(a->expert_ids, a->counts, a->offsets, cursors, a->route_pos, sorted_route,
+                         routes, a->experts, ctx.stream);
+  if (err != hipSuccess) return device_status(err, "chain route preparation launch failed");
+  err = kern::chain_grouped_mfma(a->x, a->expert_weights, a->offsets, sorted_route,
+                                 a->route_weights, a->x_permuted, a->y_permuted, a->y, a->tokens,
+                                 a->experts, a->hidden, a->output, ctx.stream);
+  return device_status(err, "chain grouped GEMM launch failed");
 }
 
 rr_status run_chain(const rr_chain_args* a, const rr_runtime_context* context,
@@ -62,6 +102,11 @@ rr_status run_chain(const rr_chain_args* a, const rr_runtime_context* context,
   // ids do not carry across stages); auto and naive pass through unchanged.
   rr_kernel_selection kernel = a->kernel;
   if (kernel.family == RR_FAMILY_OPTIMIZED) kernel.implementation_id = RR_IMPL_GFX950_NATIVE;
+  // Same dispatch checks as the stages (architecture, family / id) before the fused path.
+  rr_dispatch_decision decision{};
+  status = dispatch_operator(RR_OP_HISTOGRAM_EXCLUSIVE_SCAN, {}, kernel, ctx.architecture, &decision);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+  if (decision.kernel.family == RR_FAMILY_OPTIMIZED) return run_fused(a, ctx, from_tokens);
 
   if (from_tokens) {
     rr_dense_gemm_args dense{};

@@ -1,19 +1,21 @@
 // FP32 GEMMs on gfx950 matrix cores (v_mfma_f32_16x16x4_f32).
 //
-// One persistent kernel serves both the router dense GEMM (one segment of M
-// rows) and the ragged grouped GEMM (segments [offsets[e], offsets[e+1]) with
-// weights W[e]). The host never reads offsets: every workgroup loads them to
-// LDS, builds the per-expert row-tile prefix and walks the tile space
-// (row tiles of every expert x column tiles) with a grid-stride loop.
+// One persistent kernel serves the router dense GEMM (one segment of M rows),
+// the ragged grouped GEMM (segments [offsets[e], offsets[e+1]) with weights
+// W[e]) and the two fused forms used by the chain entries. The host never
+// reads offsets: every workgroup loads them to LDS, builds the per-expert
+// row-tile prefix and walks the tile space (row tiles of every expert x column
+// tiles) with a grid-stride loop.
 //
 // Tile: BM x BN per workgroup, BK per LDS stage (16 for the large tile, 64 for
-// the small-K tiles so a K = 256 problem takes four pipeline steps instead of
-// sixteen dependent global round trips), two LDS stages plus a register
-// prefetch of the next stage. LDS holds both operands k-contiguous ([m][k] and
-// [n][k], rows padded by 4 floats) so every MFMA operand fetch is one
-// ds_read_b128 covering four consecutive MFMA k-steps. Lane l (group
-// g = l / 16, index i = l % 16) supplies A[m0 + i][k] and B[k][n0 + i] for
-// k = kk + 4g + s at MFMA step s, which is the same k for both operands.
+// short-K tiles), two LDS stages plus a register prefetch of the next stage.
+// LDS holds both operands k-contiguous ([m][k] and [n][k], rows padded by 4
+// floats) so every MFMA operand fetch is one ds_read_b128 covering four
+// consecutive MFMA k-steps. Lane l (group g = l / 16, index i = l % 16)
+// supplies A[m0 + i][k] and B[k][n0 + i] for k = kk + 4g + s at MFMA step s,
+// which is the same k for both operands. The k order of the accumulation does
+// not depend on the tile shape, so every tile configuration (and every fused
+// form) produces bit-identical products.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -23,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "gate.h"
 #include "launchers.h"
 #include "raggedroute_capi.h"
 #include "wave.h"
@@ -32,8 +35,39 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kGroupM = 8;    // row tiles per swizzle group
-constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dispatched round-robin
+constexpr int kGroupM = 8;  // row tiles per swizzle group
+constexpr int kXcds = 8;    // MI355X: 8 XCDs, workgroups dispatched round-robin
+
+enum Mode : int {
+  kDense = 0,         // one segment [0, dense_rows), weights W
+  kGrouped = 1,       // segments from offsets, weights W[e]
+  kChainGrouped = 2,  // grouped with A rows gathered through sorted_route, x_permuted
+                      // written, and the top-2 unpermute folded into the epilogue
+  kRouterGate = 3,    // dense with the top-2 gate in the epilogue (needs N <= BN)
+};
+
+struct GemmParams {
+  const float* X;
+  const float* W;
+  const int32_t* offsets;
+  float* Y;
+  int experts;
+  int dense_rows;
+  int K;
+  int N;
+  // kChainGrouped: segment row r holds token sorted_route[r] / 2 of X; the
+  // gathered rows go to x_permuted and y_out[token] += route_weights[route] * Y[r].
+  const int32_t* sorted_route;
+  const float* route_weights;
+  float* x_permuted;
+  float* y_out;
+  // kRouterGate: top-2 ids / weights of every row over its N logits, and the
+  // rows' [y_cols]-wide slice of y_zero zeroed for the chain's accumulation.
+  int32_t* gate_ids;
+  float* gate_weights;
+  float* y_zero;
+  int y_cols;
+};
 
 template <int BM_, int BN_, int WM_, int WN_, int BK_>
 struct TileShape {
@@ -60,32 +94,34 @@ struct TileShape {
 
 // Global -> register staging of one BK slice. A rows are k-contiguous in
 // global memory; B rows are n-contiguous and are transposed on the LDS store.
+// src_rows (LDS, optional) maps tile row r to its source row of A (-1: none);
+// without it tile row r is row row0 + r, valid below row_end.
 template <class S, bool VEC>
 struct Stage {
   float a[S::kALoads][4];
   float b[S::kBLoads][4];
 
   __device__ __forceinline__ void load(const float* __restrict__ A, const float* __restrict__ B,
-                                       int row0, int row_end, int n0, int N, int K, int k0,
-                                       int tid) {
+                                       const int32_t* src_rows, int row0, int row_end, int n0,
+                                       int N, int K, int k0, int tid) {
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int r = f / (S::BK / 4);   // BK / 4 float4 per row
+      const int r = f / (S::BK / 4);  // BK / 4 float4 per row
       const int c = (f % (S::BK / 4)) * 4;
-      const int row = row0 + r;
+      const int src = src_rows != nullptr ? src_rows[r] : (row0 + r < row_end ? row0 + r : -1);
       const int k = k0 + c;
-      const float* src = A + static_cast<std::size_t>(row) * K + k;
+      const float* ptr = A + static_cast<std::size_t>(src < 0 ? 0 : src) * K + k;
       if (VEC) {
-        if (row < row_end && k < K) {
-          const float4 v = *reinterpret_cast<const float4*>(src);
+        if (src >= 0 && k < K) {
+          const float4 v = *reinterpret_cast<const float4*>(ptr);
           a[p][0] = v.x; a[p][1] = v.y; a[p][2] = v.z; a[p][3] = v.w;
         } else {
           a[p][0] = a[p][1] = a[p][2] = a[p][3] = 0.0F;
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[p][j] = (row < row_end && k + j < K) ? src[j] : 0.0F;
+        for (int j = 0; j < 4; ++j) a[p][j] = (src >= 0 && k + j < K) ? ptr[j] : 0.0F;
       }
     }
 #pragma unroll
@@ -95,17 +131,17 @@ struct Stage {
       const int n = (f / S::BK) * 4;
       const int k = k0 + kr;
       const int col = n0 + n;
-      const float* src = B + static_cast<std::size_t>(k) * N + col;
+      const float* ptr = B + static_cast<std::size_t>(k) * N + col;
       if (VEC) {
         if (k < K && col < N) {
-          const float4 v = *reinterpret_cast<const float4*>(src);
+          const float4 v = *reinterpret_cast<const float4*>(ptr);
           b[p][0] = v.x; b[p][1] = v.y; b[p][2] = v.z; b[p][3] = v.w;
         } else {
           b[p][0] = b[p][1] = b[p][2] = b[p][3] = 0.0F;
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[p][j] = (k < K && col + j < N) ? src[j] : 0.0F;
+        for (int j = 0; j < 4; ++j) b[p][j] = (k < K && col + j < N) ? ptr[j] : 0.0F;
       }
     }
   }
@@ -130,6 +166,29 @@ struct Stage {
       for (int j = 0; j < 4; ++j) Bs[(n + j) * S::kLd + kr] = b[p][j];
     }
   }
+
+  // Writes the staged A slice to rows [row0, row0 + BM) of out (the gathered
+  // x_permuted rows of the chain), valid rows and columns only.
+  __device__ __forceinline__ void store_a_rows(float* __restrict__ out, const int32_t* src_rows,
+                                               int row0, int K, int k0, int tid) const {
+#pragma unroll
+    for (int p = 0; p < S::kALoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int r = f / (S::BK / 4);
+      const int c = (f % (S::BK / 4)) * 4;
+      const int k = k0 + c;
+      if (src_rows[r] < 0) continue;
+      float* ptr = out + static_cast<std::size_t>(row0 + r) * K + k;
+      if (VEC) {
+        if (k < K) *reinterpret_cast<float4*>(ptr) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (k + j < K) ptr[j] = a[p][j];
+        }
+      }
+    }
+  }
 };
 
 // Tile space decode: row tiles are grouped kGroupM at a time so that workgroups
@@ -144,23 +203,25 @@ __device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles,
   *ct = within / rows_in_group;
 }
 
-// GROUPED = false: one dense segment of dense_rows rows with weights W (the
-// router GEMM); true: ragged segments from offsets with weights W[e].
-template <class S, bool VEC, bool GROUPED>
-__global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
-    const float* __restrict__ X, const float* __restrict__ W, const int32_t* __restrict__ offsets,
-    float* __restrict__ Y, int experts, int dense_rows, int K, int N) {
+template <class S, bool VEC, int MODE>
+__global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams prm) {
+  constexpr bool kGroupedRows = MODE == kGrouped || MODE == kChainGrouped;
   extern __shared__ float lds[];
-  float* stages = lds;                                                       // kStages stages
-  int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * S::kStageFloats);  // [experts + 1]
-  int32_t* s_pre = s_off + experts + 1;                             // [experts + 1]
+  float* stages = lds;                                                              // kStages
+  int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * S::kStageFloats);  // [E + 1]
+  int32_t* s_pre = s_off + prm.experts + 1;                                          // [E + 1]
+  int32_t* s_src = s_pre + prm.experts + 1;  // [BM] chain: token row of X per tile row
+  float* s_w = reinterpret_cast<float*>(s_src + S::BM);  // [BM] chain: route weight per tile row
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = rr::dev::lane_id();
   const int wave = tid >> 6;
+  const int experts = prm.experts;
+  const int K = prm.K;
+  const int N = prm.N;
 
   // ---- device-side scheduler: per-expert row-tile prefix in LDS ----
   for (int e = tid; e <= experts; e += S::kThreads) {
-    s_off[e] = GROUPED ? offsets[e] : (e == 0 ? 0 : dense_rows);
+    s_off[e] = kGroupedRows ? prm.offsets[e] : (e == 0 ? 0 : prm.dense_rows);
   }
   __syncthreads();
   if (wave == 0) {
@@ -216,7 +277,27 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
     const int row0 = s_off[e] + (rt - s_pre[e]) * S::BM;
     const int row_end = s_off[e + 1];
     const int n0 = ct * S::BN;
-    const float* B = W + static_cast<std::size_t>(GROUPED ? e : 0) * K * N;
+    const float* B = prm.W + static_cast<std::size_t>(kGroupedRows ? e : 0) * K * N;
+
+    const int32_t* src_rows = nullptr;
+    if constexpr (MODE == kChainGrouped) {
+      __syncthreads();  // the previous tile's epilogue is done with s_src / s_w
+      for (int r = tid; r < S::BM; r += S::kThreads) {
+        const int row = row0 + r;
+        int32_t token = -1;
+        float w = 0.0F;
+        if (row < row_end) {
+          const int32_t route = prm.sorted_route[row];
+          token = route >> 1;  // top-2: route = 2 * token + rank
+          w = prm.route_weights[route];
+        }
+        s_src[r] = token;
+        s_w[r] = w;
+      }
+      __syncthreads();
+      src_rows = s_src;
+    }
+    const bool write_xp = MODE == kChainGrouped && ct == 0;
 
     v4f acc[S::kTM][S::kTN];
 #pragma unroll
@@ -226,13 +307,16 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
 
     Stage<S, VEC> st;
     if (nk > 0) {
-      st.load(X, B, row0, row_end, n0, N, K, 0, tid);
+      st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, 0, tid);
       st.store(stages, tid);
+      if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, 0, tid);
     }
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
-      if (S::kStages > 1 && kt + 1 < nk) st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+      if (S::kStages > 1 && kt + 1 < nk) {
+        st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+      }
       const float* As = cur;
       const float* Bs = cur + S::BM * S::kLd;
 #pragma unroll
@@ -259,26 +343,92 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(
       }
       if (S::kStages > 1 && kt + 1 < nk) {
         st.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
+        if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, (kt + 1) * S::BK, tid);
       } else if (S::kStages == 1 && kt + 1 < nk) {
         __syncthreads();  // every wave is done with the single stage
-        st.load(X, B, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+        st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
         st.store(stages, tid);
+        if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, (kt + 1) * S::BK, tid);
       }
       __syncthreads();
     }
 
-    // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
+    if constexpr (MODE == kRouterGate) {
+      // Logit tile -> LDS (stage memory is free after the final barrier), then
+      // the logits are stored row-contiguous and every row's top-2 is taken by
+      // 16 lanes over its N columns.
+      constexpr int kLdT = S::BN + 1;
+      static_assert(S::BM * kLdT <= S::kStageFloats, "logit tile exceeds the stage");
+      float* tile = stages;
 #pragma unroll
-    for (int i = 0; i < S::kTM; ++i) {
+      for (int i = 0; i < S::kTM; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + wm0 + i * 16 + 4 * g + r;
-        if (row >= row_end) continue;
-        float* yrow = Y + static_cast<std::size_t>(row) * N;
+        for (int j = 0; j < S::kTN; ++j)
 #pragma unroll
-        for (int j = 0; j < S::kTN; ++j) {
-          const int col = n0 + wn0 + j * 16 + li;
-          if (col < N) yrow[col] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r)
+            tile[(wm0 + i * 16 + 4 * g + r) * kLdT + wn0 + j * 16 + li] = acc[i][j][r];
+      __syncthreads();
+      const int rows = row_end - row0 < S::BM ? row_end - row0 : S::BM;
+      for (int idx = tid; idx < rows * N; idx += S::kThreads) {
+        const int r = idx / N;
+        const int c = idx - r * N;
+        prm.Y[static_cast<std::size_t>(row0 + r) * N + c] = tile[r * kLdT + c];
+      }
+      constexpr int kRowsPerPass = S::kThreads / 16;
+      for (int r0 = 0; r0 < S::BM; r0 += kRowsPerPass) {
+        const int r = r0 + tid / 16;
+        const int sub = tid & 15;
+        uint64_t k1 = 0, k2 = 0;
+        if (r < rows) {
+          for (int c = sub; c < N; c += 16) {
+            rr::dev::insert_key(rr::dev::gate_key(tile[r * kLdT + c], c), k1, k2);
+          }
+        }
+        rr::dev::merge_top2<16>(k1, k2);
+        if (sub == 0 && r < rows) {
+          float w1, w2;
+          rr::dev::gate_weights(k1, k2, &w1, &w2);
+          const std::size_t row = static_cast<std::size_t>(row0 + r);
+          prm.gate_ids[2 * row] = rr::dev::key_expert(k1);
+          prm.gate_ids[2 * row + 1] = rr::dev::key_expert(k2);
+          prm.gate_weights[2 * row] = w1;
+          prm.gate_weights[2 * row + 1] = w2;
+        }
+      }
+      if (prm.y_zero != nullptr) {
+        float* base = prm.y_zero + static_cast<std::size_t>(row0) * prm.y_cols;
+        for (long i = tid; i < static_cast<long>(rows) * prm.y_cols; i += S::kThreads) base[i] = 0.0F;
+      }
+      __syncthreads();  // the next tile's prologue reuses the stage memory
+    } else {
+      // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
+#pragma unroll
+      for (int i = 0; i < S::kTM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rl = wm0 + i * 16 + 4 * g + r;
+          const int row = row0 + rl;
+          if (row >= row_end) continue;
+          float* yrow = prm.Y + static_cast<std::size_t>(row) * N;
+          float* comb = nullptr;
+          float w = 0.0F;
+          if constexpr (MODE == kChainGrouped) {
+            comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
+            w = s_w[rl];
+          }
+#pragma unroll
+          for (int j = 0; j < S::kTN; ++j) {
+            const int col = n0 + wn0 + j * 16 + li;
+            if (col < N) {
+              yrow[col] = acc[i][j][r];
+              if constexpr (MODE == kChainGrouped) {
+                // Both routes of a token add into the zeroed output: fl(0 + a) + b
+                // is the same in either order, so the combine is deterministic
+                // and equals the rank-order unpermute.
+                unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
+              }
+            }
+          }
         }
       }
     }
@@ -315,35 +465,28 @@ hipError_t allow_full_lds(Kernel kernel) {
   return status;
 }
 
-template <class S, bool VEC, bool GROUPED>
-hipError_t launch_one(dim3 grid, std::size_t lds, const float* x, const float* w,
-                      const int32_t* offsets, float* y, int experts, int dense_rows, int K, int N,
-                      hipStream_t stream) {
-  const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, GROUPED>);
+template <class S, bool VEC, int MODE>
+hipError_t launch_one(dim3 grid, std::size_t lds, const GemmParams& prm, hipStream_t stream) {
+  const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, MODE>);
   if (attr != hipSuccess) return attr;
-  rr_gemm_mfma_kernel<S, VEC, GROUPED><<<grid, S::kThreads, lds, stream>>>(x, w, offsets, y, experts,
-                                                                           dense_rows, K, N);
+  rr_gemm_mfma_kernel<S, VEC, MODE><<<grid, S::kThreads, lds, stream>>>(prm);
   return hipGetLastError();
 }
 
-template <class S>
-hipError_t launch_gemm(const float* x, const float* w, const int32_t* offsets, float* y,
-                       int experts, int dense_rows, int K, int N, long tile_bound,
-                       hipStream_t stream) {
-  const bool vec = (K % 4 == 0) && (N % 4 == 0) && aligned16(x) && aligned16(w);
+template <class S, int MODE>
+hipError_t launch_gemm(const GemmParams& prm, long tile_bound, hipStream_t stream) {
+  const bool vec = (prm.K % 4 == 0) && (prm.N % 4 == 0) && aligned16(prm.X) && aligned16(prm.W) &&
+                   (MODE != kChainGrouped || aligned16(prm.x_permuted));
   const long cap = static_cast<long>(device_cu_count()) * 2;
   long grid = tile_bound < cap ? tile_bound : cap;
   if (grid >= kXcds) grid = grid / kXcds * kXcds;
   if (grid < 1) grid = 1;
   const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) +
-                          2 * static_cast<std::size_t>(experts + 1) * sizeof(int32_t);
+                          2 * static_cast<std::size_t>(prm.experts + 1) * sizeof(int32_t) +
+                          2 * static_cast<std::size_t>(S::BM) * sizeof(int32_t);
   const dim3 g(static_cast<unsigned>(grid));
-  if (offsets != nullptr) {
-    return vec ? launch_one<S, true, true>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream)
-               : launch_one<S, false, true>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream);
-  }
-  return vec ? launch_one<S, true, false>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream)
-             : launch_one<S, false, false>(g, lds, x, w, offsets, y, experts, dense_rows, K, N, stream);
+  return vec ? launch_one<S, true, MODE>(g, lds, prm, stream)
+             : launch_one<S, false, MODE>(g, lds, prm, stream);
 }
 
 // 128x128, four 64x64 waves, BK 16: large problems (C4, C5 grouped).
@@ -352,8 +495,10 @@ using TileLarge = TileShape<128, 128, 2, 2, 16>;
 using TileSmall = TileShape<64, 64, 2, 2, 64>;
 // 32x64, four 16x32 waves, BK 64: small ragged segments (tens of rows per expert).
 using TileMedium = TileShape<32, 64, 2, 2, 64>;
-// 16x64, four 16x16 waves side by side, BK 64: narrow router GEMMs (N = E).
+// 16x64, four 16x16 waves side by side, BK 64: narrow router GEMMs (N = E <= 64).
 using TileNarrow = TileShape<16, 64, 1, 4, 64>;
+// 16x128, four 16x32 waves side by side, BK 64: router GEMMs with 64 < E <= 128.
+using TileNarrowWide = TileShape<16, 128, 1, 4, 64>;
 
 // Whole-K tiles (K <= 256): one LDS stage holds all of K.
 using TileSmallK256 = TileShape<64, 64, 2, 2, 256>;    // 133 KB LDS
@@ -362,7 +507,7 @@ using TileNarrowK256 = TileShape<16, 64, 1, 4, 256>;   // 83 KB LDS
 
 // Tile override for tuning sweeps: RR_GEMM_TILE = large | small | medium |
 // narrow | small256 | medium256 | narrow256 forces one of the (equally
-// correct) tile configurations.
+// correct) tile configurations of the dense and grouped GEMMs.
 int tile_override() {
   static const int choice = [] {
     const char* v = std::getenv("RR_GEMM_TILE");
@@ -391,51 +536,52 @@ long tile_estimate(long rows, int segments, int bm, int n, int bn) {
   return (ceil_div(rows, bm) + segments) * ceil_div(n, bn);
 }
 
-hipError_t gemm_dispatch(const float* x, const float* w, const int32_t* offsets, float* y,
-                         int experts, int dense_rows, int K, int N, long rows_per_expert,
-                         long total_rows_estimate, hipStream_t stream) {
+template <class S, int MODE>
+hipError_t launch_tile(const GemmParams& prm, long rows_per_expert, hipStream_t stream) {
+  const int segments = MODE == kDense || MODE == kRouterGate ? 1 : prm.experts;
+  return launch_gemm<S, MODE>(prm, tile_bound(segments, rows_per_expert, S::BM, prm.N, S::BN),
+                              stream);
+}
+
+template <int MODE>
+hipError_t gemm_dispatch(const GemmParams& prm, long rows_per_expert, long total_rows_estimate,
+                         hipStream_t stream) {
   const long cus = device_cu_count();
-  const int segments = offsets != nullptr ? experts : 0;
+  const int segments = MODE == kDense ? 0 : prm.experts;
+  const int n = prm.N;
   switch (tile_override()) {
-    case 1:
-      return launch_gemm<TileLarge>(x, w, offsets, y, experts, dense_rows, K, N,
-                                    tile_bound(experts, rows_per_expert, TileLarge::BM, N, TileLarge::BN), stream);
-    case 2:
-      return launch_gemm<TileSmall>(x, w, offsets, y, experts, dense_rows, K, N,
-                                    tile_bound(experts, rows_per_expert, TileSmall::BM, N, TileSmall::BN), stream);
-    case 3:
-      return launch_gemm<TileMedium>(x, w, offsets, y, experts, dense_rows, K, N,
-                                     tile_bound(experts, rows_per_expert, TileMedium::BM, N, TileMedium::BN), stream);
-    case 4:
-      return launch_gemm<TileNarrow>(x, w, offsets, y, experts, dense_rows, K, N,
-                                     tile_bound(experts, rows_per_expert, TileNarrow::BM, N, TileNarrow::BN), stream);
-    case 5:
-      return launch_gemm<TileSmallK256>(x, w, offsets, y, experts, dense_rows, K, N,
-                                        tile_bound(experts, rows_per_expert, 64, N, 64), stream);
-    case 6:
-      return launch_gemm<TileMediumK256>(x, w, offsets, y, experts, dense_rows, K, N,
-                                         tile_bound(experts, rows_per_expert, 32, N, 64), stream);
-    case 7:
-      return launch_gemm<TileNarrowK256>(x, w, offsets, y, experts, dense_rows, K, N,
-                                         tile_bound(experts, rows_per_expert, 16, N, 64), stream);
-    default:
-      break;
+    case 1: return launch_tile<TileLarge, MODE>(prm, rows_per_expert, stream);
+    case 2: return launch_tile<TileSmall, MODE>(prm, rows_per_expert, stream);
+    case 3: return launch_tile<TileMedium, MODE>(prm, rows_per_expert, stream);
+    case 4: return launch_tile<TileNarrow, MODE>(prm, rows_per_expert, stream);
+    case 5: return launch_tile<TileSmallK256, MODE>(prm, rows_per_expert, stream);
+    case 6: return launch_tile<TileMediumK256, MODE>(prm, rows_per_expert, stream);
+    case 7: return launch_tile<TileNarrowK256, MODE>(prm, rows_per_expert, stream);
+    default: break;
   }
   // Largest tile that still gives every CU work (two tiles per CU for the
   // large tile, whose LDS and registers allow two resident workgroups).
-  if (tile_estimate(total_rows_estimate, segments, TileLarge::BM, N, TileLarge::BN) >= 2 * cus) {
-    return launch_gemm<TileLarge>(
-        x, w, offsets, y, experts, dense_rows, K, N,
-        tile_bound(experts, rows_per_expert, TileLarge::BM, N, TileLarge::BN), stream);
+  if (tile_estimate(total_rows_estimate, segments, TileLarge::BM, n, TileLarge::BN) >= 2 * cus) {
+    return launch_tile<TileLarge, MODE>(prm, rows_per_expert, stream);
   }
-  if (tile_estimate(total_rows_estimate, segments, TileSmall::BM, N, TileSmall::BN) >= cus) {
-    return launch_gemm<TileSmall>(
-        x, w, offsets, y, experts, dense_rows, K, N,
-        tile_bound(experts, rows_per_expert, TileSmall::BM, N, TileSmall::BN), stream);
+  if (tile_estimate(total_rows_estimate, segments, TileSmall::BM, n, TileSmall::BN) >= cus) {
+    return launch_tile<TileSmall, MODE>(prm, rows_per_expert, stream);
   }
-  return launch_gemm<TileNarrow>(
-      x, w, offsets, y, experts, dense_rows, K, N,
-      tile_bound(experts, rows_per_expert, TileNarrow::BM, N, TileNarrow::BN), stream);
+  return launch_tile<TileNarrow, MODE>(prm, rows_per_expert, stream);
+}
+
+GemmParams base_params(const float* x, const float* w, const int32_t* offsets, float* y,
+                       int experts, int dense_rows, int K, int N) {
+  GemmParams p{};
+  p.X = x;
+  p.W = w;
+  p.offsets = offsets;
+  p.Y = y;
+  p.experts = experts;
+  p.dense_rows = dense_rows;
+  p.K = K;
+  p.N = N;
+  return p;
 }
 
 }  // namespace
@@ -443,7 +589,7 @@ hipError_t gemm_dispatch(const float* x, const float* w, const int32_t* offsets,
 hipError_t dense_gemm_mfma(const float* a, const float* b, float* c, int m, int n, int k,
                            hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
-  return gemm_dispatch(a, b, nullptr, c, 1, m, k, n, m, m, stream);
+  return gemm_dispatch<kDense>(base_params(a, b, nullptr, c, 1, m, k, n), m, m, stream);
 }
 
 hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offsets, float* y,
@@ -452,9 +598,37 @@ hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offs
   if (max_expert_tokens <= 0 || output <= 0) return hipSuccess;
   // The host never reads offsets; the caller's bound sizes the grid and the
   // device scheduler covers every row of every segment.
-  const long total_estimate = max_expert_tokens;
-  return gemm_dispatch(x, w, offsets, y, experts, 0, hidden, output, max_expert_tokens,
-                       total_estimate, stream);
+  return gemm_dispatch<kGrouped>(
+      base_params(x, w, offsets, y, experts, 0, hidden, output), max_expert_tokens,
+      max_expert_tokens, stream);
+}
+
+hipError_t router_gate_mfma(const float* x, const float* router_weights, float* logits,
+                            int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
+                            int tokens, int experts, int hidden, hipStream_t stream) {
+  if (tokens <= 0) return hipSuccess;
+  if (experts > 128) return hipErrorInvalidValue;
+  GemmParams p = base_params(x, router_weights, nullptr, logits, 1, tokens, hidden, experts);
+  p.gate_ids = ids;
+  p.gate_weights = gate_weights;
+  p.y_zero = y_zero;
+  p.y_cols = y_cols;
+  if (experts <= 64) return launch_tile<TileNarrow, kRouterGate>(p, tokens, stream);
+  return launch_tile<TileNarrowWide, kRouterGate>(p, tokens, stream);
+}
+
+hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const int32_t* offsets,
+                              const int32_t* sorted_route, const float* route_weights,
+                              float* x_permuted, float* y_permuted, float* y, int tokens,
+                              int experts, int hidden, int output, hipStream_t stream) {
+  if (tokens <= 0 || output <= 0) return hipSuccess;
+  GemmParams p = base_params(x, expert_weights, offsets, y_permuted, experts, 0, hidden, output);
+  p.sorted_route = sorted_route;
+  p.route_weights = route_weights;
+  p.x_permuted = x_permuted;
+  p.y_out = y;
+  const long routes = 2L * tokens;
+  return gemm_dispatch<kChainGrouped>(p, routes, routes, stream);
 }
 
 }  // namespace rr::kern

@@ -18,9 +18,25 @@ hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offs
                              int experts, int hidden, int output, int max_expert_tokens,
                              hipStream_t stream);
 
+// ---- fused chain forms (gemm.hip) ----
+// logits = x * router_weights with each row's top-2 ids / weights taken in the
+// epilogue; rows [0, tokens) of y_zero ([tokens, y_cols]) are zeroed. E <= 128.
+hipError_t router_gate_mfma(const float* x, const float* router_weights, float* logits,
+                            int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
+                            int tokens, int experts, int hidden, hipStream_t stream);
+// Grouped GEMM over x rows gathered through sorted_route (top-2 routes): writes
+// x_permuted and y_permuted, and adds w[route] * y_permuted[row] into the
+// zeroed y[token] (the unpermute).
+hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const int32_t* offsets,
+                              const int32_t* sorted_route, const float* route_weights,
+                              float* x_permuted, float* y_permuted, float* y, int tokens,
+                              int experts, int hidden, int output, hipStream_t stream);
+
 // ---- routing kernels (routing.hip) ----
+// y_zero (optional): [tokens, y_cols] rows zeroed by the same launch (chain fusion).
 hipError_t topk_gate_wave(const float* logits, int32_t* ids, float* weights, int tokens,
-                          int experts, hipStream_t stream);
+                          int experts, hipStream_t stream, float* y_zero = nullptr,
+                          int y_cols = 0);
 // counts[e] = #{ids == e}; overwrites counts (no external reset needed).
 hipError_t histogram_native(const int32_t* ids, int32_t* counts, int route_pairs, int experts,
                             hipStream_t stream);
@@ -35,6 +51,14 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
                                 int32_t* cursors, float* x_permuted, int32_t* route_pos,
                                 int32_t* sorted_route, int tokens, int experts, int top_k,
                                 int hidden, hipStream_t stream);
+// Fused-chain route preparation: ids -> counts, offsets, stable route_pos,
+// sorted_route (required here) and cursors in one launch.
+hipError_t route_prep(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* cursors,
+                      int32_t* route_pos, int32_t* sorted_route, int routes, int experts,
+                      hipStream_t stream);
+// Token-owned row copy x -> x_permuted through route_pos (second half of token_permute).
+hipError_t permute_copy(const float* x, const int32_t* route_pos, float* x_permuted, int tokens,
+                        int top_k, int hidden, hipStream_t stream);
 hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
                             const float* route_weights, float* y, int tokens, int top_k,
                             int output, hipStream_t stream);

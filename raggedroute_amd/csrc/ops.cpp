@@ -55,9 +55,12 @@ size_t rr_token_permute_workspace_size(const rr_token_permute_args* args) {
 }
 size_t rr_grouped_gemm_workspace_size(const rr_grouped_gemm_args*) { return 0; }
 size_t rr_unpermute_workspace_size(const rr_unpermute_args*) { return 0; }
+// Chain workspace: E int32 cursor words, then 2T int32 words that hold
+// sorted_route when the caller passes none (used by the fused path).
 size_t rr_chain_workspace_size(const rr_chain_args* args) {
-  if (args == nullptr || args->experts <= 0) return 0;
-  return static_cast<size_t>(args->experts) * sizeof(int32_t);
+  if (args == nullptr || args->experts <= 0 || args->tokens < 0) return 0;
+  return (static_cast<size_t>(args->experts) + 2 * static_cast<size_t>(args->tokens)) *
+         sizeof(int32_t);
 }
 
 // reference src/dense_gemm/operator.cpp:18-58

@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "gate.h"
 #include "launchers.h"
 #include "raggedroute_capi.h"
 #include "wave.h"
@@ -29,48 +30,14 @@ constexpr int kWavesPerBlock = kBlock / 64;
 constexpr int kSingleBlockRoutes = 65536;
 
 // ============================================================================
-// Top-2 gate: selected softmax over the two largest logits of each row.
-// Semantics of reference src/topk_gate/cuda_naive/baseline.cu:18-80: order by
-// (value desc, expert asc); NaN ranks as -Inf; -0 and +0 tie (lower id wins);
-// equal selected values -> {0.5, 0.5}; +Inf first or -Inf second -> {1, 0};
-// else r = exp(v2 - v1), w1 = 1 / (1 + r), w2 = r * w1. An all-NaN row
-// therefore yields ids {0, 1} with weights {0.5, 0.5} without a special case.
+// Top-2 gate (semantics and key encoding in gate.h).
 // ============================================================================
 
-// Packed key: larger key = better candidate. High word: order-preserving bits
-// of the value (NaN -> -Inf, -0 -> +0); low word: ~expert so ties prefer the
-// lower expert id. A zero key is below every real key.
-__device__ __forceinline__ uint64_t gate_key(float value, int expert) {
-  uint32_t bits = __float_as_uint(isnan(value) ? -INFINITY : value);
-  if ((bits << 1) == 0u) bits = 0u;
-  const uint32_t ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return (static_cast<uint64_t>(ordered) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(expert));
-}
-
-__device__ __forceinline__ float key_value(uint64_t key) {
-  const uint32_t ordered = static_cast<uint32_t>(key >> 32);
-  const uint32_t bits = (ordered & 0x80000000u) ? (ordered & 0x7FFFFFFFu) : ~ordered;
-  return __uint_as_float(bits);
-}
-
-__device__ __forceinline__ int key_expert(uint64_t key) {
-  return static_cast<int>(~static_cast<uint32_t>(key));
-}
-
-__device__ __forceinline__ void insert_key(uint64_t key, uint64_t& k1, uint64_t& k2) {
-  if (key > k1) {
-    k2 = k1;
-    k1 = key;
-  } else if (key > k2) {
-    k2 = key;
-  }
-}
-
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
-  const int lo = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), mask, 64);
-  const int hi = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), mask, 64);
-  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
-}
+using rr::dev::gate_key;
+using rr::dev::gate_weights;
+using rr::dev::insert_key;
+using rr::dev::key_expert;
+using rr::dev::merge_top2;
 
 // LPR lanes cooperate on one row (LPR in 1..64, a power of two); each lane
 // keeps a local top-2 and the row's lanes merge with an xor butterfly.
@@ -78,7 +45,9 @@ template <int LPR, bool VEC4>
 __global__ __launch_bounds__(256) void rr_topk_gate_kernel(const float* __restrict__ logits,
                                                            int32_t* __restrict__ ids,
                                                            float* __restrict__ weights,
-                                                           int tokens, int experts) {
+                                                           int tokens, int experts,
+                                                           float* __restrict__ y_zero,
+                                                           int y_cols) {
   constexpr int kRowsPerWave = 64 / LPR;
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
@@ -100,47 +69,37 @@ __global__ __launch_bounds__(256) void rr_topk_gate_kernel(const float* __restri
       for (int e = sub; e < experts; e += LPR) insert_key(gate_key(p[e], e), k1, k2);
     }
   }
-#pragma unroll
-  for (int d = LPR / 2; d >= 1; d >>= 1) {
-    const uint64_t o1 = shfl_xor_u64(k1, d);
-    const uint64_t o2 = shfl_xor_u64(k2, d);
-    const uint64_t hi = k1 > o1 ? k1 : o1;
-    const uint64_t lo = k1 > o1 ? o1 : k1;
-    const uint64_t m2 = k2 > o2 ? k2 : o2;
-    k2 = lo > m2 ? lo : m2;
-    k1 = hi;
-  }
+  merge_top2<LPR>(k1, k2);
   if (sub == 0 && row < tokens) {
-    const float v1 = key_value(k1);
-    const float v2 = key_value(k2);
     float w1, w2;
-    if (v1 == v2) {
-      w1 = 0.5F;
-      w2 = 0.5F;
-    } else if (v1 == INFINITY || v2 == -INFINITY) {
-      w1 = 1.0F;
-      w2 = 0.0F;
-    } else {
-      const float r = expf(v2 - v1);
-      w1 = 1.0F / (1.0F + r);
-      w2 = __fmul_rn(r, w1);
-    }
+    gate_weights(k1, k2, &w1, &w2);
     ids[2 * row] = key_expert(k1);
     ids[2 * row + 1] = key_expert(k2);
     weights[2 * row] = w1;
     weights[2 * row + 1] = w2;
   }
+  // Chain fusion: zero the combined output rows of this block's tokens so the
+  // fused grouped GEMM can accumulate both routes of a token into them.
+  if (y_zero != nullptr) {
+    constexpr int kRowsPerBlock = 4 * kRowsPerWave;
+    const long first = static_cast<long>(blockIdx.x) * kRowsPerBlock;
+    const long rows = tokens - first < kRowsPerBlock ? tokens - first : kRowsPerBlock;
+    float* base = y_zero + first * y_cols;
+    for (long i = threadIdx.x; i < rows * y_cols; i += blockDim.x) base[i] = 0.0F;
+  }
 }
 
 template <int LPR>
 hipError_t launch_gate(const float* logits, int32_t* ids, float* weights, int tokens, int experts,
-                       bool vec4, hipStream_t stream) {
+                       bool vec4, float* y_zero, int y_cols, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 * (64 / LPR);
   const unsigned blocks = static_cast<unsigned>((tokens + kRowsPerBlock - 1) / kRowsPerBlock);
   if (vec4) {
-    rr_topk_gate_kernel<LPR, true><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts);
+    rr_topk_gate_kernel<LPR, true><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts,
+                                                               y_zero, y_cols);
   } else {
-    rr_topk_gate_kernel<LPR, false><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts);
+    rr_topk_gate_kernel<LPR, false><<<blocks, 256, 0, stream>>>(logits, ids, weights, tokens, experts,
+                                                                y_zero, y_cols);
   }
   return hipGetLastError();
 }
@@ -389,6 +348,123 @@ __global__ __launch_bounds__(WAVES * 64) void rr_permute_rank_kernel(
   }
 }
 
+// Route preparation for the fused chain: ids -> counts, offsets, stable
+// route_pos, sorted_route and cursors in one launch. Block b ranks routes
+// [b*chunk, (b+1)*chunk) like rr_permute_rank_kernel, but derives the offsets
+// itself: it counts every route per expert (routes before its chunk give the
+// stable base, all routes give the totals) and scans the totals in LDS, so no
+// block waits for another. LDS: (WAVES + 2) * E + 1 + 16 ints.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void rr_route_prep_kernel(
+    const int32_t* __restrict__ ids, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ cursors, int32_t* __restrict__ route_pos,
+    int32_t* __restrict__ sorted_route, int routes, int experts, int bits, int chunk) {
+  constexpr int kThreads = WAVES * 64;
+  extern __shared__ int32_t lds[];
+  int32_t* wc = lds;                       // [WAVES][experts]
+  int32_t* base = wc + WAVES * experts;    // [experts]: earlier routes of each expert
+  int32_t* soff = base + experts;          // [experts + 1]: segment offsets
+  int32_t* wsum = soff + experts + 1;      // [16]
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int begin = static_cast<int>(blockIdx.x) * chunk;
+  const int end = begin + chunk < routes ? begin + chunk : routes;
+
+  for (int i = tid; i < WAVES * experts; i += kThreads) wc[i] = 0;
+  __syncthreads();
+  wave_count_ids(wc + wave * experts, ids, 0, begin, experts, bits, wave, WAVES);
+  __syncthreads();
+  for (int e = tid; e < experts; e += kThreads) {
+    int32_t sum = 0;
+    for (int w = 0; w < WAVES; ++w) {
+      sum += wc[w * experts + e];
+      wc[w * experts + e] = 0;
+    }
+    base[e] = sum;
+  }
+  __syncthreads();
+  wave_count_ids(wc + wave * experts, ids, begin, routes, experts, bits, wave, WAVES);
+  __syncthreads();
+  for (int e = tid; e < experts; e += kThreads) {
+    int32_t sum = base[e];
+    for (int w = 0; w < WAVES; ++w) {
+      sum += wc[w * experts + e];
+      wc[w * experts + e] = 0;
+    }
+    soff[e] = sum;  // total count; scanned in place below
+  }
+  __syncthreads();
+  // Exclusive scan of the totals: thread t owns `per` consecutive experts.
+  {
+    const int per = (experts + kThreads - 1) / kThreads;
+    int32_t local = 0;
+    for (int j = 0; j < per; ++j) {
+      const int e = tid * per + j;
+      if (e < experts) local += soff[e];
+    }
+    const int32_t incl_wave = wave_inclusive_scan(local);
+    if (lane == 63) wsum[wave] = incl_wave;
+    __syncthreads();
+    if (wave == 0) {
+      int32_t v = lane < WAVES ? wsum[lane] : 0;
+      v = wave_inclusive_scan(v);
+      if (lane < WAVES) wsum[lane] = v;
+    }
+    __syncthreads();
+    int32_t run = (wave > 0 ? wsum[wave - 1] : 0) + incl_wave - local;
+    for (int j = 0; j < per; ++j) {
+      const int e = tid * per + j;
+      if (e < experts) {
+        const int32_t c = soff[e];
+        soff[e] = run;
+        run += c;
+      }
+    }
+    if (tid == 0) soff[experts] = wsum[WAVES - 1];
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int e = tid; e < experts; e += kThreads) {
+      const int32_t c = soff[e + 1] - soff[e];
+      counts[e] = c;
+      cursors[e] = c;
+      offsets[e] = soff[e];
+    }
+    if (tid == 0) offsets[experts] = soff[experts];
+  }
+
+  for (int sub = begin; sub < end; sub += kThreads) {
+    const int r = sub + tid;
+    const int id = r < end ? ids[r] : -1;
+    const bool valid = id >= 0 && id < experts;
+    const uint64_t active = __ballot(valid);
+    const uint64_t mask = match_mask(static_cast<uint32_t>(valid ? id : 0), bits, active);
+    const int rank = __popcll(mask & lanemask_lt());
+    const bool leader = valid && rank == 0;
+    if (leader) wc[wave * experts + id] = __popcll(mask);
+    __syncthreads();
+    for (int e = tid; e < experts; e += kThreads) {
+      int32_t running = base[e];
+      for (int w = 0; w < WAVES; ++w) {
+        const int32_t c = wc[w * experts + e];
+        if (c != 0) {
+          wc[w * experts + e] = running;
+          running += c;
+        }
+      }
+      base[e] = running;
+    }
+    __syncthreads();
+    if (r < end) {
+      const int32_t pos = valid ? soff[id] + wc[wave * experts + id] + rank : -1;
+      route_pos[r] = pos;
+      if (pos >= 0) sorted_route[pos] = r;
+    }
+    if (leader) wc[wave * experts + id] = 0;
+  }
+}
+
 // Token-owned row copy: element (t, c) of x is read once and stored to every
 // valid destination row of token t. VEC4: c indexes float4 columns.
 template <bool VEC4>
@@ -480,20 +556,20 @@ unsigned stream_grid(uint64_t items) {
 }  // namespace
 
 hipError_t topk_gate_wave(const float* logits, int32_t* ids, float* weights, int tokens,
-                          int experts, hipStream_t stream) {
+                          int experts, hipStream_t stream, float* y_zero, int y_cols) {
   if (tokens <= 0) return hipSuccess;
   const bool vec4 = (experts % 4 == 0) && aligned16(logits);
   const int per_lane_units = vec4 ? experts / 4 : (experts + 3) / 4;
   int lpr = 1;
   while (lpr < per_lane_units && lpr < 64) lpr <<= 1;
   switch (lpr) {
-    case 1: return launch_gate<1>(logits, ids, weights, tokens, experts, vec4, stream);
-    case 2: return launch_gate<2>(logits, ids, weights, tokens, experts, vec4, stream);
-    case 4: return launch_gate<4>(logits, ids, weights, tokens, experts, vec4, stream);
-    case 8: return launch_gate<8>(logits, ids, weights, tokens, experts, vec4, stream);
-    case 16: return launch_gate<16>(logits, ids, weights, tokens, experts, vec4, stream);
-    case 32: return launch_gate<32>(logits, ids, weights, tokens, experts, vec4, stream);
-    default: return launch_gate<64>(logits, ids, weights, tokens, experts, vec4, stream);
+    case 1: return launch_gate<1>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    case 2: return launch_gate<2>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    case 4: return launch_gate<4>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    case 8: return launch_gate<8>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    case 16: return launch_gate<16>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    case 32: return launch_gate<32>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
+    default: return launch_gate<64>(logits, ids, weights, tokens, experts, vec4, y_zero, y_cols, stream);
   }
 }
 
@@ -558,6 +634,46 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || hidden == 0) return err;
+  const bool vec4 = (hidden % 4 == 0) && aligned16(x) && aligned16(x_permuted);
+  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? hidden / 4 : hidden);
+  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
+  if (vec4) {
+    rr_permute_copy_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
+        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+  } else {
+    rr_permute_copy_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
+        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+  }
+  return hipGetLastError();
+}
+
+hipError_t route_prep(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* cursors,
+                      int32_t* route_pos, int32_t* sorted_route, int routes, int experts,
+                      hipStream_t stream) {
+  if (routes <= 0) return hipSuccess;
+  const bool wide = experts > 512;
+  const int threads = wide ? 512 : 1024;
+  int chunk = threads;
+  if (routes > 64 * threads) chunk = ((routes + 63) / 64 + threads - 1) / threads * threads;
+  const int blocks = (routes + chunk - 1) / chunk;
+  const std::size_t lds =
+      ((static_cast<std::size_t>(threads / 64) + 2) * experts + 1 + kWavesPerBlock) * sizeof(int32_t);
+  if (wide) {
+    rr_route_prep_kernel<8><<<blocks, threads, lds, stream>>>(ids, counts, offsets, cursors, route_pos,
+                                                              sorted_route, routes, experts,
+                                                              bits_for(experts), chunk);
+  } else {
+    rr_route_prep_kernel<16><<<blocks, threads, lds, stream>>>(ids, counts, offsets, cursors, route_pos,
+                                                               sorted_route, routes, experts,
+                                                               bits_for(experts), chunk);
+  }
+  return hipGetLastError();
+}
+
+hipError_t permute_copy(const float* x, const int32_t* route_pos, float* x_permuted, int tokens,
+                        int top_k, int hidden, hipStream_t stream) {
+  const int routes = tokens * top_k;
+  if (routes <= 0 || hidden <= 0) return hipSuccess;
   const bool vec4 = (hidden % 4 == 0) && aligned16(x) && aligned16(x_permuted);
   const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? hidden / 4 : hidden);
   if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;

@@ -183,3 +183,72 @@ def test_chain_from_logits_route_trace(ctx, device, kat):
         dev = ChainRun(cfg, inp, device).run(ctx)
         assert np.array_equal(dev["ids"], desired), frame
         check_chain(cfg, inp, dev)
+
+
+def run_stages(cfg, inp, device, ctx):
+    """The seven public operators one by one (native kernels), as the
+    reference chain_adapter enqueues them."""
+    t, e, k, n = cfg.tokens, cfg.experts, cfg.hidden, cfg.output
+    native = rr.kernel(rr.KernelFamily.kOptimized, rr.GFX950_NATIVE)
+    dev = lambda a: a if isinstance(a, torch.Tensor) else to_dev(a, device)  # noqa: E731
+    x, we = dev(inp["x"]), dev(inp["expert_weights"])
+    i32 = dict(dtype=torch.int32, device=device)
+    logits = torch.empty(t, e, device=device) if cfg.from_tokens else dev(inp["logits"])
+    ids, w = torch.empty(t, 2, **i32), torch.empty(t, 2, device=device)
+    counts, offsets = torch.empty(e, **i32), torch.empty(e + 1, **i32)
+    xp, pos, inv = torch.empty(2 * t, k, device=device), torch.empty(2 * t, **i32), torch.empty(2 * t, **i32)
+    yp, y, cursors = torch.empty(2 * t, n, device=device), torch.empty(t, n, device=device), torch.empty(e, **i32)
+
+    def ok(status):
+        assert status.ok(), status.message
+    if cfg.from_tokens:
+        wr = dev(inp["router_weights"])
+        ok(rr.dense_gemm(rr.DenseGemmArgs(a=rr.cview(x.data_ptr()), b=rr.cview(wr.data_ptr()),
+                                          c=rr.mview(logits.data_ptr()), m=t, n=e, k=k, kernel=native), ctx))
+    ok(rr.topk_gate(rr.TopKGateArgs(logits=rr.cview(logits.data_ptr()), expert_ids=ids.data_ptr(),
+                                    weights=rr.mview(w.data_ptr()), tokens=t, experts=e, kernel=native), ctx))
+    ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
+        expert_ids=ids.data_ptr(), counts=counts.data_ptr(), offsets=offsets.data_ptr(), route_pairs=2 * t,
+        experts=e, kernel=native), ctx))
+    pctx = rr.RuntimeContext(stream=ctx.stream, workspace=cursors.data_ptr(), workspace_bytes=4 * e,
+                             architecture=ctx.architecture)
+    ok(rr.token_permute(rr.TokenPermuteArgs(
+        x=rr.cview(x.data_ptr()), expert_ids=ids.data_ptr(), offsets=offsets.data_ptr(),
+        x_permuted=rr.mview(xp.data_ptr()), route_pos=pos.data_ptr(), sorted_route=inv.data_ptr(), tokens=t,
+        experts=e, top_k=2, hidden=k, kernel=native), pctx))
+    ok(rr.grouped_gemm(rr.GroupedGemmArgs(
+        x_permuted=rr.cview(xp.data_ptr()), expert_weights=rr.cview(we.data_ptr()), offsets=offsets.data_ptr(),
+        y_permuted=rr.mview(yp.data_ptr()), experts=e, hidden=k, output=n, max_expert_tokens=2 * t,
+        kernel=native), ctx))
+    ok(rr.unpermute(rr.UnpermuteArgs(
+        y_permuted=rr.cview(yp.data_ptr()), route_pos=pos.data_ptr(), route_weights=rr.cview(w.data_ptr()),
+        y=rr.mview(y.data_ptr()), tokens=t, top_k=2, output=n, kernel=native), ctx))
+    torch.cuda.synchronize()
+    return {"logits": to_host(logits), "ids": to_host(ids), "weights": to_host(w), "counts": to_host(counts),
+            "offsets": to_host(offsets), "route_pos": to_host(pos), "sorted_route": to_host(inv),
+            "x_permuted": to_host(xp), "y_permuted": to_host(yp), "y": to_host(y), "cursors": to_host(cursors)}
+
+
+@pytest.mark.parametrize("shape", [
+    ("tokens", 5, 4, 7, 5), ("tokens", 512, 32, 256, 64), ("tokens", 4096, 64, 256, 128),
+    ("tokens", 1000, 128, 96, 40), ("tokens", 777, 256, 64, 33), ("tokens", 300, 1024, 20, 12),
+    ("logits", 4096, 64, 256, 128), ("logits", 333, 7, 13, 9),
+])
+@pytest.mark.parametrize("with_inverse", [True, False])
+def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):
+    """The fused chain (three launches) writes every output of the seven stages
+    bit-identically to the operators run one by one."""
+    kind, t, e, k, n = shape
+    cfg = workloads.ChainConfig("fused", t, e, k, n, from_tokens=kind == "tokens")
+    inp = workloads.chain_inputs(cfg, seed=3)
+    run = ChainRun(cfg, inp, device, with_inverse=with_inverse)
+    fused = run.run(ctx)
+    fused["cursors"] = to_host(run.ws[:e])
+    ref = run_stages(cfg, inp, device, ctx)
+    for key in ("logits", "ids", "weights", "counts", "offsets", "route_pos", "x_permuted", "y_permuted",
+                "y", "cursors") + (("sorted_route",) if with_inverse else ()):
+        a, b = fused[key], ref[key]
+        assert a.shape == b.shape, key
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), f"{key} differs"
+    check_chain(cfg, inp, fused)

@@ -249,7 +249,7 @@ def test_workspace_contracts():
     chain = rr.ChainArgs(tokens=4, experts=8, hidden=4, output=4, logits=addr, expert_ids=addr,
                          route_weights=addr, counts=addr, offsets=addr, route_pos=addr, y_permuted=addr,
                          y=addr, x=addr, x_permuted=addr, expert_weights=addr, router_weights=addr)
-    assert rr.get_chain_workspace_size(chain) == 32
+    assert rr.get_chain_workspace_size(chain) == (8 + 2 * 4) * 4
     assert rr.chain_from_logits(chain, ctx).code == S.kInsufficientWorkspace
     assert rr.chain_from_tokens(rr.ChainArgs(tokens=0, experts=8), ctx).ok()
 
