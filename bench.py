@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--only", default="", help="comma list of extras to run: c3,c4,c4u,c5")
+    ap.add_argument("--profile", default="", choices=["", "headline", "c4"],
+                    help="profiler driver: a fixed number of launches of one case, no timing, "
+                         "no JSON line (for rocprofv3 --pmc / --kernel-trace runs)")
     return ap.parse_args()
 
 
@@ -59,6 +62,29 @@ def work_model(t, e, k, n, active=None, sorted_route=False):
         "token_permute": (4 * t * k + 4 * r * k + 4 * r + 4 * (e + 1) + 4 * r + (4 * r if sorted_route else 0), 0.0),
         "grouped_gemm": (4 * (r * k + active * k * n + r * n) + 4 * (e + 1), 2.0 * r * k * n),
         "unpermute": (4 * r * n + 4 * t * n + 8 * r, 3.0 * t * n),
+    }
+
+
+def fused_work_model(t, e, k, n, active=None):
+    """Algorithmic bytes / flops of the fused chain's launches (unique HBM
+    traffic: every input read once, every output written once)."""
+    r = 2 * t
+    active = e if active is None else active
+    gate = (4 * (t * k + k * e + t * e) + 16 * t + 4 * t * n, 2.0 * t * k * e)
+    prep = (4 * r + 4 * e + 4 * (e + 1) + 4 * e + 8 * r, 0.0)
+    gemm = (4 * (t * k + active * k * n + r * k + r * n + t * n) + 8 * r + 4 * (e + 1),
+            2.0 * r * k * n + 2.0 * r * n)
+    return {
+        # x, router weights in; logits, ids, weights out; y zeroed
+        "router_gate": gate,
+        "gate": (gate[0] - 4 * (t * k + k * e) + 0, 0.0),
+        # ids in; counts, offsets, cursors, route_pos, sorted_route out
+        "route_prep": prep,
+        # x, active expert weights, sorted_route, route weights, offsets in;
+        # x_permuted, y_permuted, y out (y += w * y_permuted)
+        "expert_gemm": gemm,
+        # both in one launch: ids in instead of sorted_route
+        "route_prep_expert_gemm": (prep[0] + gemm[0] - 8 * r, gemm[1]),
     }
 
 
@@ -140,6 +166,11 @@ class Chain:
         if not status.ok():
             raise RuntimeError(status.message)
 
+    def fused_launch(self, index):
+        status = self.rr.chain_fused_launch(self.chain_args, self.ctx, self.cfg.from_tokens, index)
+        if not status.ok():
+            raise RuntimeError(f"fused launch {index}: {status.message}")
+
     def stage(self, name):
         fn, args = self.stage_args[name]
         status = fn(args, self.ctx)
@@ -166,6 +197,17 @@ def stage_report(torch, ch, reps, model):
     out = {}
     for name in ch.stage_args:
         sec = time_loop(torch, lambda: ch.stage(name), reps)
+        nbytes, flops = model[name]
+        out[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "flops": flops,
+                     "roofline": roofline(name, nbytes, flops, sec)}
+    return out
+
+
+def launch_report(torch, ch, reps, model):
+    """Each launch of the fused chain alone (what chain_from_* runs)."""
+    out = {}
+    for index, name in enumerate(ch.rr.chain_fused_launch_names(ch.chain_args, ch.cfg.from_tokens)):
+        sec = time_loop(torch, lambda: ch.fused_launch(index), reps)
         nbytes, flops = model[name]
         out[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "flops": flops,
                      "roofline": roofline(name, nbytes, flops, sec)}
@@ -199,13 +241,16 @@ def headline(torch, device, args):
         b.synchronize()
         spans.append(a.elapsed_time(b) / 1e3)
     active = int((ch.counts.cpu().numpy() > 0).sum())
+    launches = launch_report(torch, ch, args.stage_reps,
+                             fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
+    ch.chain()  # restore y (timing launch 2 alone keeps adding into it)
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, ch, args.stage_reps, model)
     return cfg, ch, inputs, {"elapsed_s": elapsed, "wall_s": wall, "p50_s": statistics.median(spans),
-                             "stages": stages, "active_experts": active}
+                             "launches": launches, "stages": stages, "active_experts": active}
 
 
-def c4(torch, device, hidden=4096, output=14336, reps=5):
+def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50):
     """Mixtral-shaped ragged grouped GEMM + permute + unpermute: T=8192, R=16384,
     E=8 with 7 active (Zipf 1.2), expert 7 empty."""
     import raggedroute_amd as rr
@@ -228,7 +273,7 @@ def c4(torch, device, hidden=4096, output=14336, reps=5):
     active = int((ch.counts.cpu().numpy() > 0).sum())
     model = work_model(t, e, hidden, output, active)
     out = {"T": t, "E": e, "K": hidden, "N": output, "active_experts": active}
-    for name, n_reps in (("token_permute", 50), ("grouped_gemm", reps), ("unpermute", 50)):
+    for name, n_reps in (("token_permute", stage_reps), ("grouped_gemm", reps), ("unpermute", stage_reps)):
         sec = time_loop(torch, lambda: ch.stage(name), n_reps, warmup=1)
         nbytes, flops = model[name]
         out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
@@ -245,11 +290,14 @@ def c5(torch, device, steps=20):
     ch = Chain(cfg, inputs, device)
     sec = time_loop(torch, ch.chain, steps, warmup=3)
     active = int((ch.counts.cpu().numpy() > 0).sum())
+    launches = launch_report(torch, ch, 10,
+                             fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, ch, 10, model)
     del ch, inputs
     torch.cuda.empty_cache()
-    return {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1), "stages": stages}
+    return {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1),
+            "launches": launches, "stages": stages}
 
 
 def c3(torch, device):
@@ -286,6 +334,36 @@ def cpu_baseline(inputs_host, budget_s):
     return statistics.median(runs), len(runs)
 
 
+def profile(torch, device, case):
+    """Fixed launch sequence for counter runs: first a plain 64 MiB copy (three
+    launches, the calibration of FETCH_SIZE / WRITE_SIZE), then the case."""
+    from raggedroute_amd import workloads
+    src = torch.ones(16 << 20, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print("profile: copy calibration done (3 x 64 MiB)", flush=True)
+    if case == "headline":
+        cfg = workloads.HEADLINE
+        ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
+        for _ in range(5):
+            ch.chain()
+        torch.cuda.synchronize()
+        for index in range(3):
+            for _ in range(3):
+                ch.fused_launch(index)
+        for name in ch.stage_args:
+            for _ in range(3):
+                ch.stage(name)
+        torch.cuda.synchronize()
+        print("profile: headline done (5 chains, 3 x each fused launch, 3 x each stage)", flush=True)
+    elif case == "c4":
+        c4(torch, device, reps=2, stage_reps=2)
+        print("profile: c4 done", flush=True)
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -298,11 +376,14 @@ def main() -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.profile:
+        profile(torch, device, args.profile)
+        return 0
     cfg, ch, inputs, head = headline(torch, device, args)
     tokens_per_s = cfg.tokens * args.steps / head["elapsed_s"]
-    stages = head["stages"]
-    dominant = max(stages, key=lambda s: stages[s]["us"])
-    roof = dict(stages[dominant]["roofline"])
+    launches = head["launches"]
+    dominant = max(launches, key=lambda s: launches[s]["us"])
+    roof = dict(launches[dominant]["roofline"])
     roof["kernel"] = dominant
     roof["traffic"] = None
     traffic_file = REPO / "profiles" / f"{dominant}_headline_traffic.json"
@@ -348,7 +429,8 @@ def main() -> int:
                    "N": cfg.output, "top_k": 2, "active_experts": head["active_experts"]},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "stages": stages,
+        "launches": launches,
+        "stages": head["stages"],
         "extras": extras,
     }
     print(json.dumps(line))

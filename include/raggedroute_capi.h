@@ -299,6 +299,21 @@ rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* 
  * sequence of reference benchmarks/adapters/chain_adapter.cpp:263-467. */
 rr_status rr_chain_from_tokens(const rr_chain_args* args, const rr_runtime_context* context);
 rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_context* context);
+/* No reference counterpart: timing hook. Runs one launch of the fused
+ * (auto / optimized) chain alone so that a profiler or benchmark can time it
+ * with events on the context's stream. Launches are numbered in execution
+ * order; their number (2 or 3) depends on the shape, and an index past the
+ * last one returns RR_STATUS_INVALID_ARGUMENT. Launch 0 is the router GEMM +
+ * top-2 gate (the gate only when from_tokens is 0) and zeroes y; the last
+ * launch adds into y, so repeating it alone keeps accumulating. Same argument
+ * checks as the chain. */
+rr_status rr_chain_fused_launch(const rr_chain_args* args, const rr_runtime_context* context,
+                                int32_t from_tokens, int32_t launch);
+/* No reference counterpart: name of fused launch `launch` for this shape
+ * ("router_gate", "gate", "route_prep", "expert_gemm",
+ * "route_prep_expert_gemm"), or NULL past the last launch. */
+const char* rr_chain_fused_launch_name(const rr_chain_args* args, int32_t from_tokens,
+                                       int32_t launch);
 
 /* ---- dispatch (reference include/raggedroute/dispatch.h:12-46) ---- */
 

@@ -53,7 +53,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libraggedroute_amd.so"
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"{LIB_PATH} is missing: build it with `python -m raggedroute_amd.build` "
+            f"{LIB_PATH} is missing: build it with `python raggedroute_amd/build.py` "
             "(there is no non-HIP fallback)"
         )
     return bind(ctypes.CDLL(str(LIB_PATH)))
@@ -107,6 +107,23 @@ def chain_from_tokens(args: ChainArgs, context: RuntimeContext | None = None) ->
 
 def chain_from_logits(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
     return lib.rr_chain_from_logits(byref(args), byref(_ctx(context)))
+
+
+def chain_fused_launch(args: ChainArgs, context: RuntimeContext | None, from_tokens: bool,
+                       launch: int) -> Status:
+    """One launch of the fused chain alone (numbered in execution order), for
+    per-launch timing."""
+    return lib.rr_chain_fused_launch(byref(args), byref(_ctx(context)), int(bool(from_tokens)), launch)
+
+
+def chain_fused_launch_names(args: ChainArgs, from_tokens: bool) -> list[str]:
+    """Names of the fused chain's launches for this shape, in execution order."""
+    names = []
+    while True:
+        name = lib.rr_chain_fused_launch_name(byref(args), int(bool(from_tokens)), len(names))
+        if name is None:
+            return names
+        names.append(name.decode())
 
 
 # ---- workspace queries (reference operators.h:114-122) ----

@@ -301,6 +301,8 @@ PROTOTYPES += [
     ("rr_chain_workspace_size", c_size_t, [POINTER(ChainArgs)]),
     ("rr_chain_from_tokens", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_from_logits", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
+    ("rr_chain_fused_launch", Status, [POINTER(ChainArgs), POINTER(RuntimeContext), c_int32, c_int32]),
+    ("rr_chain_fused_launch_name", c_char_p, [POINTER(ChainArgs), c_int32, c_int32]),
     ("rr_classify_compute_capability", c_int32, [c_int32, c_int32]),
     ("rr_classify_gcn_arch_name", c_int32, [c_char_p]),
     ("rr_query_current_device_architecture", Status, [i32p]),

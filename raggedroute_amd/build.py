@@ -5,7 +5,10 @@ sources (*.cpp) with g++ against the HIP headers. Objects go to _build/ at the
 repository root and the shared library is written in-tree next to this file so
 that it travels with the repository snapshot.
 
-    python -m raggedroute_amd.build          # full rebuild
+    python raggedroute_amd/build.py          # full rebuild
+
+Run it as a script (or load it by path): importing the package loads the
+library, which does not exist yet on a fresh checkout.
 """
 from __future__ import annotations
 

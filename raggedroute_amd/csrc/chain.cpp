@@ -4,13 +4,16 @@
 // dense GEMM -> top-2 gate -> histogram+scan -> token permute -> grouped GEMM
 // -> unpermute, all on the caller's stream, with no host synchronisation.
 //
-// Auto / optimized family: three fused launches that write every output of the
-// seven stages with the same values as running them one by one:
+// Auto / optimized family: two or three fused launches that write every output
+// of the seven stages with the same values as running them one by one:
 //   1. router GEMM with the top-2 gate in its epilogue (gate kernel for
 //      chain_from_logits), also zeroing y;
 //   2. route preparation: counts, offsets, stable route_pos, sorted_route, cursors;
 //   3. grouped GEMM gathering x rows through sorted_route, writing x_permuted
 //      and y_permuted and adding both weighted routes of each token into y.
+// Where the narrow-output strip kernel covers the shape (N <= 128, K <= 256,
+// T <= 8192, E <= 256), 2 and 3 are one launch: every workgroup derives the
+// offsets and its own rows' routes from the ids itself.
 // Naive family: the seven stages through the public C ABI entries (the grouped
 // GEMM gets the worst-case launch bound max_expert_tokens = R, reference
 // chain_adapter.cpp:391-401).
@@ -60,33 +63,72 @@ rr_status validate_chain(const rr_chain_args* a, const rr_runtime_context* conte
   return ok_status();
 }
 
-// Fused path (auto / optimized family); see the file comment.
-rr_status run_fused(const rr_chain_args* a, const rr_runtime_context& ctx, bool from_tokens) noexcept {
+// Fused path (auto / optimized family); see the file comment. Launches in
+// order: 0 = router GEMM + gate (gate only for chain_from_logits); then, when
+// the strip kernel covers the shape, 1 = route preparation + expert GEMM +
+// unpermute in one launch; otherwise 1 = route preparation and 2 = expert GEMM
+// + unpermute.
+bool merged_prep(const rr_chain_args* a) noexcept {
+  return kern::strip_chain_ok(a->tokens, a->experts, a->hidden, a->output, a->x, a->expert_weights,
+                              a->expert_ids, a->x_permuted);
+}
+
+int fused_launch_count(const rr_chain_args* a) noexcept { return merged_prep(a) ? 2 : 3; }
+
+const char* fused_launch_name(const rr_chain_args* a, bool from_tokens, int launch) noexcept {
+  const bool merged = merged_prep(a);
+  if (launch == 0) return from_tokens ? "router_gate" : "gate";
+  if (launch == 1) return merged ? "route_prep_expert_gemm" : "route_prep";
+  if (launch == 2 && !merged) return "expert_gemm";
+  return nullptr;
+}
+
+// `only` selects a single launch for per-launch timing, -1 runs all of them.
+rr_status run_fused(const rr_chain_args* a, const rr_runtime_context& ctx, bool from_tokens,
+                    int only = -1) noexcept {
   auto* cursors = static_cast<int32_t*>(ctx.workspace);
   int32_t* sorted_route = a->sorted_route != nullptr ? a->sorted_route : cursors + a->experts;
   const int routes = a->tokens * 2;
+  const bool merged = merged_prep(a);
   hipError_t err = hipSuccess;
-  if (from_tokens && a->experts <= 128) {
-    err = kern::router_gate_mfma(a->x, a->router_weights, a->logits, a->expert_ids,
-                                 a->route_weights, a->y, a->output, a->tokens, a->experts,
-                                 a->hidden, ctx.stream);
-  } else {
-    if (from_tokens) {
-      err = kern::dense_gemm_mfma(a->x, a->router_weights, a->logits, a->tokens, a->experts,
-                                  a->hidden, ctx.stream);
-      if (err != hipSuccess) return device_status(err, "chain router GEMM launch failed");
+  if (only < 0 || only == 0) {
+    if (from_tokens && a->experts <= 128) {
+      err = kern::router_gate_mfma(a->x, a->router_weights, a->logits, a->expert_ids,
+                                   a->route_weights, a->y, a->output, a->tokens, a->experts,
+                                   a->hidden, ctx.stream);
+    } else {
+      if (from_tokens) {
+        err = kern::dense_gemm_mfma(a->x, a->router_weights, a->logits, a->tokens, a->experts,
+                                    a->hidden, ctx.stream);
+        if (err != hipSuccess) return device_status(err, "chain router GEMM launch failed");
+      }
+      err = kern::topk_gate_wave(a->logits, a->expert_ids, a->route_weights, a->tokens,
+                                 a->experts, ctx.stream, a->y, a->output);
     }
-    err = kern::topk_gate_wave(a->logits, a->expert_ids, a->route_weights, a->tokens, a->experts,
-                               ctx.stream, a->y, a->output);
+    if (err != hipSuccess) return device_status(err, "chain gate launch failed");
   }
-  if (err != hipSuccess) return device_status(err, "chain gate launch failed");
-  err = kern::route_prep(a->expert_ids, a->counts, a->offsets, cursors, a->route_pos, sorted_route,
-                         routes, a->experts, ctx.stream);
-  if (err != hipSuccess) return device_status(err, "chain route preparation launch failed");
-  err = kern::chain_grouped_mfma(a->x, a->expert_weights, a->offsets, sorted_route,
-                                 a->route_weights, a->x_permuted, a->y_permuted, a->y, a->tokens,
-                                 a->experts, a->hidden, a->output, ctx.stream);
-  return device_status(err, "chain grouped GEMM launch failed");
+  if (merged) {
+    if (only < 0 || only == 1) {
+      err = kern::strip_chain(a->x, a->expert_weights, a->expert_ids, a->route_weights, a->counts,
+                              a->offsets, cursors, a->route_pos, a->sorted_route, a->x_permuted,
+                              a->y_permuted, a->y, a->tokens, a->experts, a->hidden, a->output,
+                              ctx.stream);
+      if (err != hipSuccess) return device_status(err, "chain expert GEMM launch failed");
+    }
+    return ok_status();
+  }
+  if (only < 0 || only == 1) {
+    err = kern::route_prep(a->expert_ids, a->counts, a->offsets, cursors, a->route_pos,
+                           sorted_route, routes, a->experts, ctx.stream);
+    if (err != hipSuccess) return device_status(err, "chain route preparation launch failed");
+  }
+  if (only < 0 || only == 2) {
+    err = kern::chain_grouped_mfma(a->x, a->expert_weights, a->offsets, sorted_route,
+                                   a->route_weights, a->x_permuted, a->y_permuted, a->y,
+                                   a->tokens, a->experts, a->hidden, a->output, ctx.stream);
+    if (err != hipSuccess) return device_status(err, "chain grouped GEMM launch failed");
+  }
+  return ok_status();
 }
 
 rr_status run_chain(const rr_chain_args* a, const rr_runtime_context* context,
@@ -199,6 +241,23 @@ rr_status rr_chain_from_tokens(const rr_chain_args* args, const rr_runtime_conte
 
 rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_context* context) {
   return rr::run_chain(args, context, false);
+}
+
+rr_status rr_chain_fused_launch(const rr_chain_args* args, const rr_runtime_context* context,
+                                int32_t from_tokens, int32_t launch) {
+  rr_status status = rr::validate_chain(args, context, from_tokens != 0);
+  if (status.code != RR_STATUS_SUCCESS) return status;
+  if (launch < 0 || launch >= rr::fused_launch_count(args)) {
+    return rr::invalid_argument("fused chain launch index out of range for this shape");
+  }
+  if (args->tokens == 0) return status;
+  return rr::run_fused(args, *context, from_tokens != 0, launch);
+}
+
+const char* rr_chain_fused_launch_name(const rr_chain_args* args, int32_t from_tokens,
+                                       int32_t launch) {
+  if (args == nullptr) return nullptr;
+  return rr::fused_launch_name(args, from_tokens != 0, launch);
 }
 
 }  // extern "C"

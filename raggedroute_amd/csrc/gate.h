@@ -13,6 +13,8 @@
 #include <cmath>
 #include <cstdint>
 
+#include "wave.h"
+
 namespace rr::dev {
 
 // Packed key: larger key = better candidate. High word: order-preserving bits
@@ -36,13 +38,15 @@ __device__ __forceinline__ int key_expert(uint64_t key) {
   return static_cast<int>(~static_cast<uint32_t>(key));
 }
 
+// Selects instead of an if / else that assigns one of two references: the
+// compiler turns the latter into a store through a selected address and moves
+// the pair to scratch memory.
 __device__ __forceinline__ void insert_key(uint64_t key, uint64_t& k1, uint64_t& k2) {
-  if (key > k1) {
-    k2 = k1;
-    k1 = key;
-  } else if (key > k2) {
-    k2 = key;
-  }
+  const bool above1 = key > k1;
+  const bool above2 = key > k2;
+  const uint64_t second = above1 ? k1 : (above2 ? key : k2);
+  k1 = above1 ? key : k1;
+  k2 = second;
 }
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
@@ -65,6 +69,39 @@ __device__ __forceinline__ void merge_top2(uint64_t& k1, uint64_t& k2) {
     k2 = lo > m2 ? lo : m2;
     k1 = hi;
   }
+}
+
+// Top-2 merge of a lane's pair with a partner lane's pair (the two pairs hold
+// distinct keys, zeros aside).
+__device__ __forceinline__ void merge_pair(uint64_t& k1, uint64_t& k2, uint64_t o1, uint64_t o2) {
+  const uint64_t hi = k1 > o1 ? k1 : o1;
+  const uint64_t lo = k1 > o1 ? o1 : k1;
+  const uint64_t m2 = k2 > o2 ? k2 : o2;
+  k2 = lo > m2 ? lo : m2;
+  k1 = hi;
+}
+
+template <int kCtrl>
+__device__ __forceinline__ uint64_t dpp_move_u64(uint64_t v) {
+  const uint32_t lo = rr::dev::dpp_move<kCtrl>(static_cast<uint32_t>(v));
+  const uint32_t hi = rr::dev::dpp_move<kCtrl>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Top-2 over the 16 lanes of each DPP row (lanes 16r .. 16r + 15) with
+// register moves only: partners xor 1 and xor 2 inside quads, then the mirror
+// inside each half row (pairs the two quads) and inside the row (pairs the
+// two halves). Every pairing joins disjoint lane sets, so every lane ends with
+// the top-2 of its row.
+__device__ __forceinline__ void merge_top2_row16(uint64_t& k1, uint64_t& k2) {
+  constexpr int kQuadXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+  constexpr int kQuadXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+  constexpr int kRowHalfMirror = 0x141;  // lane i <-> 7 - i inside 8
+  constexpr int kRowMirror = 0x140;      // lane i <-> 15 - i inside 16
+  merge_pair(k1, k2, dpp_move_u64<kQuadXor1>(k1), dpp_move_u64<kQuadXor1>(k2));
+  merge_pair(k1, k2, dpp_move_u64<kQuadXor2>(k1), dpp_move_u64<kQuadXor2>(k2));
+  merge_pair(k1, k2, dpp_move_u64<kRowHalfMirror>(k1), dpp_move_u64<kRowHalfMirror>(k2));
+  merge_pair(k1, k2, dpp_move_u64<kRowMirror>(k1), dpp_move_u64<kRowMirror>(k2));
 }
 
 // Selected-softmax weights of the two chosen keys.

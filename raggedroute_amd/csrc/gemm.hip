@@ -507,7 +507,8 @@ using TileNarrowK256 = TileShape<16, 64, 1, 4, 256>;   // 83 KB LDS
 
 // Tile override for tuning sweeps: RR_GEMM_TILE = large | small | medium |
 // narrow | small256 | medium256 | narrow256 forces one of the (equally
-// correct) tile configurations of the dense and grouped GEMMs.
+// correct) tile configurations of the dense and grouped GEMMs, also where the
+// narrow-output strip kernels (strip.hip) would otherwise run.
 int tile_override() {
   static const int choice = [] {
     const char* v = std::getenv("RR_GEMM_TILE");
@@ -589,6 +590,7 @@ GemmParams base_params(const float* x, const float* w, const int32_t* offsets, f
 hipError_t dense_gemm_mfma(const float* a, const float* b, float* c, int m, int n, int k,
                            hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
+  if (tile_override() == 0 && strip_shape_ok(k, n, a, b)) return strip_dense(a, b, c, m, n, k, stream);
   return gemm_dispatch<kDense>(base_params(a, b, nullptr, c, 1, m, k, n), m, m, stream);
 }
 
@@ -598,6 +600,10 @@ hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offs
   if (max_expert_tokens <= 0 || output <= 0) return hipSuccess;
   // The host never reads offsets; the caller's bound sizes the grid and the
   // device scheduler covers every row of every segment.
+  if (tile_override() == 0 && strip_shape_ok(hidden, output, x, w) && strip_segments_ok(experts)) {
+    return strip_grouped(x, w, offsets, y, experts, hidden, output,
+                         static_cast<long>(experts) * max_expert_tokens, stream);
+  }
   return gemm_dispatch<kGrouped>(
       base_params(x, w, offsets, y, experts, 0, hidden, output), max_expert_tokens,
       max_expert_tokens, stream);
@@ -608,6 +614,10 @@ hipError_t router_gate_mfma(const float* x, const float* router_weights, float* 
                             int tokens, int experts, int hidden, hipStream_t stream) {
   if (tokens <= 0) return hipSuccess;
   if (experts > 128) return hipErrorInvalidValue;
+  if (tile_override() == 0 && strip_shape_ok(hidden, experts, x, router_weights)) {
+    return strip_router_gate(x, router_weights, logits, ids, gate_weights, y_zero, y_cols, tokens,
+                             experts, hidden, stream);
+  }
   GemmParams p = base_params(x, router_weights, nullptr, logits, 1, tokens, hidden, experts);
   p.gate_ids = ids;
   p.gate_weights = gate_weights;

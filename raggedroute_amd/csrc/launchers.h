@@ -32,6 +32,33 @@ hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const
                               float* x_permuted, float* y_permuted, float* y, int tokens,
                               int experts, int hidden, int output, hipStream_t stream);
 
+// ---- narrow-output strip GEMMs (strip.hip): N <= 128, K <= 256 ----
+// Shape / alignment test shared by the strip entries (K and N multiples of 4,
+// 16-byte aligned A and W).
+bool strip_shape_ok(int k, int n, const void* a, const void* w);
+// Grouped strips take up to 256 segments.
+bool strip_segments_ok(int segments);
+// The fused route preparation + expert GEMM also needs T <= 8192, E <= 256 and
+// the route-id stage to fit in LDS.
+bool strip_chain_ok(int tokens, int experts, int k, int n, const void* x, const void* w,
+                    const void* ids, const void* x_permuted);
+hipError_t strip_dense(const float* a, const float* b, float* c, int m, int n, int k,
+                       hipStream_t stream);
+// rows_bound: upper bound on the total segment rows (sizes the grid only).
+hipError_t strip_grouped(const float* x, const float* w, const int32_t* offsets, float* y,
+                         int experts, int hidden, int output, long rows_bound, hipStream_t stream);
+hipError_t strip_router_gate(const float* x, const float* router_weights, float* logits,
+                             int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
+                             int tokens, int experts, int hidden, hipStream_t stream);
+// ids (top-2 routes of every token, all in [0, experts)) -> counts, offsets,
+// cursors, stable route_pos, sorted_route (optional), x_permuted, y_permuted,
+// and y += w * y_permuted (y zeroed beforehand) in one launch.
+hipError_t strip_chain(const float* x, const float* expert_weights, const int32_t* ids,
+                       const float* route_weights, int32_t* counts, int32_t* offsets,
+                       int32_t* cursors, int32_t* route_pos, int32_t* sorted_route,
+                       float* x_permuted, float* y_permuted, float* y, int tokens, int experts,
+                       int hidden, int output, hipStream_t stream);
+
 // ---- routing kernels (routing.hip) ----
 // y_zero (optional): [tokens, y_cols] rows zeroed by the same launch (chain fusion).
 hipError_t topk_gate_wave(const float* logits, int32_t* ids, float* weights, int tokens,

@@ -1,0 +1,737 @@
+// Narrow-output FP32 GEMMs on gfx950 matrix cores: 16-row strips spanning all
+// N <= 128 output columns, K <= 256 (the router GEMM and the expert GEMM of
+// the fused chain at the shapes of the reference chain benchmarks).
+//
+// Work unit: a strip = 16 rows of one segment (expert) x every output column.
+// One persistent workgroup per CU owns a contiguous range of strips; wave w
+// computes columns [16 w, 16 w + 16) of each strip (BN / 16 waves).
+//   B (the segment's [K, N] weights) is resident in LDS for as long as the
+//     workgroup stays on that segment: it is fetched with coalesced loads
+//     (each lane quad reads 64 contiguous bytes of a k row, a wave 16 rows)
+//     and transposed into
+//     [n][K + 4] rows, whose padding keeps both the transposing stores and the
+//     ds_read_b128 operand fetches free of bank conflicts.
+//   A rows (16 x K) are loaded by the whole workgroup with row-contiguous
+//     float4 accesses into registers, stored to a [16][K + 4] LDS stage, and
+//     the next strip's rows are loaded while the current strip's MFMAs run.
+// Accumulation order per output element: k chunks of 16 ascending, inside a
+// chunk MFMA step s sums k = 16c + 4g + s over g = 0..3, exactly as the tiled
+// kernel in gemm.hip does, so both produce bit-identical results.
+//
+// Modes:
+//   kStripDense      c = a * w (one segment of M rows);
+//   kStripRouterGate dense + every row's top-2 gate (ids, selected-softmax
+//                    weights) in the epilogue + zeroing of the row's y slice;
+//   kStripGrouped    segments from offsets (read on the device);
+//   kStripChain      the chain's route preparation and expert GEMM in one
+//                    launch: every workgroup holds all route ids in
+//                    registers (a quarter per wave), counts them into offsets,
+//                    compacts the routes of its own strips in stable (route
+//                    index) order with wave ballots, writes their
+//                    route_pos / sorted_route entries, gathers the token rows
+//                    of x (written to x_permuted), stores y_permuted and adds
+//                    w * y_permuted into the zeroed y (top-2: fl(0 + a) + b is
+//                    the same in either order, so the combine is deterministic
+//                    and equals the rank-order unpermute).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+#include <cstddef>
+#include <cstdint>
+
+#include "gate.h"
+#include "launchers.h"
+#include "wave.h"
+
+namespace rr::kern {
+namespace {
+
+using rr::dev::lane_id;
+using rr::dev::lanemask_lt;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 16;        // rows per strip = one MFMA tile
+constexpr int kMaxChunks = 16;   // K <= 256 in chunks of 16
+constexpr int kXcds = 8;         // MI355X: workgroups round-robin over 8 XCDs
+constexpr int kMaxRoutes = 16384; // chain: route ids held in registers
+constexpr int kMaxSegs = 8;       // chain: segments one workgroup's strips may span
+constexpr int kMaxBlocks = 4;     // segments <= 256, 64 per lane column
+
+enum StripMode : int { kStripDense = 0, kStripRouterGate = 1, kStripGrouped = 2, kStripChain = 3 };
+
+struct StripParams {
+  const float* A;  // dense / grouped: [rows, K]; chain: x [T, K] gathered by token
+  const float* W;  // [segments, K, N]
+  float* C;        // dense: [M, N]; grouped / chain: y_permuted [R, N]
+  int M;           // dense: rows; chain: routes R = 2T
+  int K;
+  int N;
+  int segments;    // 1 (dense) or experts
+  int max_strips;  // chain: LDS capacity of the per-workgroup strip table
+  const int32_t* offsets;  // grouped: [segments + 1]
+  // router gate
+  int32_t* gate_ids;
+  float* gate_weights;
+  float* y_zero;
+  int y_cols;
+  // chain
+  const int32_t* ids;
+  const float* route_weights;
+  int32_t* counts;
+  int32_t* offsets_out;
+  int32_t* cursors;
+  int32_t* route_pos;
+  int32_t* sorted_route;  // optional
+  float* x_permuted;
+  float* y;
+};
+
+// Always-issued 16-byte load (ptr is clamped in bounds by the caller) with the
+// value replaced by zeros where !valid: a load under a condition becomes a
+// branch per load and a wait at every join, serialising the loads.
+__device__ __forceinline__ v4f load_or_zero(const float* ptr, bool valid) {
+  const v4f v = *reinterpret_cast<const v4f*>(ptr);
+  return valid ? v : v4f{0.0F, 0.0F, 0.0F, 0.0F};
+}
+
+// Per-lane segment table: lane l holds segment e = 64 j + l (segments <= 256)
+// with rows [off[j], off[j] + cnt[j]) and strips [pre[j], pre[j] + strips).
+// Lookups of a uniform segment are readlanes, the strip -> segment search is a
+// ballot: no LDS round trips in the scheduling arithmetic.
+struct SegTable {
+  int32_t cnt[kMaxBlocks];
+  int32_t off[kMaxBlocks];
+  int32_t pre[kMaxBlocks];
+  int32_t total_strips;
+};
+
+__device__ __forceinline__ int32_t strips_of(int32_t rows) { return (rows + kRows - 1) / kRows; }
+
+// cnt[] set (zero past the last segment) -> off[], pre[], total_strips.
+// Every lane of the wave takes part.
+__device__ __forceinline__ void seg_scan(SegTable& t, int nblk) {
+  int32_t carry_rows = 0, carry_strips = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxBlocks; ++j) {
+    if (j < nblk) {
+      const int32_t st = strips_of(t.cnt[j]);
+      const int32_t ri = rr::dev::wave_inclusive_scan(t.cnt[j]);
+      const int32_t si = rr::dev::wave_inclusive_scan(st);
+      t.off[j] = carry_rows + ri - t.cnt[j];
+      t.pre[j] = carry_strips + si - st;
+      carry_rows += __builtin_amdgcn_readlane(ri, 63);
+      carry_strips += __builtin_amdgcn_readlane(si, 63);
+    }
+  }
+  t.total_strips = carry_strips;
+}
+
+// Value of a per-lane table column for the uniform segment e.
+__device__ __forceinline__ int32_t seg_field(const int32_t (&col)[kMaxBlocks], int e) {
+  int32_t v = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxBlocks; ++j) {
+    if (j == (e >> 6)) v = __builtin_amdgcn_readlane(col[j], e & 63);
+  }
+  return v;
+}
+
+// Segment of strip s: the last segment whose first strip is <= s (it is never
+// empty, since an empty segment shares its first strip with the next one).
+__device__ __forceinline__ int seg_find(const SegTable& t, int nblk, int segments, int s) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = kMaxBlocks - 1; j >= 0; --j) {
+    if (j < nblk) {
+      const uint64_t m = __ballot(64 * j + lane < segments && t.pre[j] <= s);
+      if (m != 0) return 64 * j + 63 - __builtin_clzll(m);
+    }
+  }
+  return 0;
+}
+
+struct StripInfo {
+  int e;        // segment
+  int row0;     // first row of the strip (segment order)
+  int row_end;  // end of the segment's rows
+  int rank0;    // rank of row0 inside the segment
+};
+
+__device__ __forceinline__ StripInfo strip_info(const SegTable& t, int nblk, int segments, int s) {
+  StripInfo si;
+  si.e = seg_find(t, nblk, segments, s);
+  const int off = seg_field(t.off, si.e);
+  si.rank0 = (s - seg_field(t.pre, si.e)) * kRows;
+  si.row0 = off + si.rank0;
+  si.row_end = off + seg_field(t.cnt, si.e);
+  return si;
+}
+
+// One wave per 16 output columns: BN = 128 -> 8 waves, BN = 64 -> 4 waves.
+template <int BN>
+constexpr int strip_threads() { return BN / 16 * 64; }
+
+template <int BN, int MODE, int CHUNKS>
+__global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(StripParams p) {
+  constexpr int kWaves = BN / 16;
+  constexpr int kThreads = kWaves * 64;
+  constexpr int kNB = BN / 16;                         // 16-column blocks of B
+  constexpr int kBLoads = kMaxChunks * kNB / kWaves;   // float4 B loads per lane (whole K)
+  constexpr int kIdChunks = kMaxRoutes / 256 / kWaves; // route-id chunks per wave
+  constexpr int kRowThreads = kThreads / kRows;        // A staging: threads per row
+  constexpr int kALoads = 64 / kRowThreads;            // float4 per thread (K <= 256)
+  static_assert(BN == 64 || BN == 128, "BN is 64 or 128");
+  extern __shared__ __align__(16) float lds[];
+
+  const int K = p.K;
+  const int N = p.N;
+  const int E = p.segments;
+  const int nblk = (E + 63) >> 6;
+  const int chunks = CHUNKS > 0 ? CHUNKS : (K + 15) >> 4;
+  const int kLd = chunks * 16 + 4;
+  float* Bs = lds;                // [BN][kLd]: B of the current segment, k contiguous
+  float* As = Bs + BN * kLd;      // [16][kLd]: A rows of the current strip
+  uint64_t* s_keys = reinterpret_cast<uint64_t*>(As + kRows * kLd);  // router: [waves][16][2]
+  int32_t* s_cnt =
+      reinterpret_cast<int32_t*>(s_keys + (MODE == kStripRouterGate ? kWaves * kRows * 2 : 0));
+  int32_t* s_misc = s_cnt + kMaxBlocks * 64;    // [waves][kMaxSegs]
+  int32_t* s_slot = s_misc + kWaves * kMaxSegs; // chain: [max_strips * 16] route of each row
+  float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
+
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int li = lane & 15;
+  const int grid = static_cast<int>(gridDim.x);
+  const int b = static_cast<int>(blockIdx.x);
+  // Consecutive workers on one XCD: the workgroups of one segment share its
+  // weights through the same L2.
+  const int worker = (grid % kXcds == 0) ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
+
+  // ---- B of a segment: whole K in registers, then transposed into LDS ----
+  // Four consecutive lanes read one contiguous 64-byte row segment (the
+  // memory pipeline merges a quad's accesses); a wave load covers 16 k rows.
+  v4f breg[kBLoads];
+  const int bks = lane >> 2;
+  const int bnq = lane & 3;
+  auto load_b = [&](int e) {
+    const float* W = p.W + static_cast<std::size_t>(e) * K * N;
+#pragma unroll
+    for (int u = 0; u < kBLoads; ++u) {
+      const int blk = wave + kWaves * u;
+      const int k = (blk / kNB) * 16 + bks;
+      const int n = (blk % kNB) * 16 + 4 * bnq;
+      const int kc = k < K ? k : K - 1;
+      const int nc = n < N ? n : N - 4;
+      breg[u] = load_or_zero(W + static_cast<std::size_t>(kc) * N + nc, k < K && n < N);
+    }
+  };
+  auto store_b = [&]() {
+#pragma unroll
+    for (int u = 0; u < kBLoads; ++u) {
+      const int blk = wave + kWaves * u;
+      if (blk < chunks * kNB) {
+        const int k = (blk / kNB) * 16 + bks;
+        const int n = (blk % kNB) * 16 + 4 * bnq;
+        float* dst = Bs + n * kLd + k;
+        dst[0] = breg[u].x;
+        dst[kLd] = breg[u].y;
+        dst[2 * kLd] = breg[u].z;
+        dst[3 * kLd] = breg[u].w;
+      }
+    }
+  };
+  if constexpr (MODE == kStripDense || MODE == kStripRouterGate) load_b(0);
+
+  // ---------------------------------------------------------------- segments
+  SegTable tab;
+  // Chain: wave w keeps route-id chunks [c_begin, c_end) of 256 routes in
+  // registers (lane l holds routes 256c + 4l .. + 3); they feed the histogram
+  // here and the route compaction below.
+  int4 idv[kIdChunks];
+  int c_begin = 0, c_end = 0;
+  if constexpr (MODE == kStripChain) {
+    const int R = p.M;
+    const int nchunks = (R + 255) >> 8;
+    c_begin = wave * nchunks / kWaves;
+    c_end = (wave + 1) * nchunks / kWaves;
+    for (int e = tid; e < kMaxBlocks * 64; e += kThreads) s_cnt[e] = 0;
+#pragma unroll
+    for (int u = 0; u < kIdChunks; ++u) {
+      const int r = (c_begin + u) * 256 + 4 * lane;
+      const bool full = c_begin + u < c_end && r + 3 < R;
+      const int4 v = *reinterpret_cast<const int4*>(p.ids + (full ? r : 0));
+      idv[u] = full ? v : make_int4(-1, -1, -1, -1);
+      if (c_begin + u < c_end && r < R && r + 3 >= R) {  // the ragged tail (R % 4 != 0)
+        idv[u].x = p.ids[r];
+        if (r + 1 < R) idv[u].y = p.ids[r + 1];
+        if (r + 2 < R) idv[u].z = p.ids[r + 2];
+      }
+    }
+    __syncthreads();  // counts zeroed
+#pragma unroll
+    for (int u = 0; u < kIdChunks; ++u) {
+      if (c_begin + u < c_end) {
+        const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (static_cast<unsigned>(vals[k]) < static_cast<unsigned>(E)) atomicAdd(s_cnt + vals[k], 1);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) tab.cnt[j] = j < nblk ? s_cnt[64 * j + lane] : 0;
+  } else if constexpr (MODE == kStripGrouped) {
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      const int e = 64 * j + lane;
+      const int ec = e < E ? e : E - 1;
+      const int32_t lo = p.offsets[ec];
+      const int32_t hi = p.offsets[ec + 1];
+      tab.cnt[j] = (j < nblk && e < E) ? hi - lo : 0;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) tab.cnt[j] = (j == 0 && lane == 0) ? p.M : 0;
+  }
+  seg_scan(tab, nblk);
+  if constexpr (MODE == kStripGrouped) {
+    // rows keep the caller's offsets (the same as the prefix of the counts for
+    // well-formed offsets; the caller's base is honoured)
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      const int e = 64 * j + lane;
+      tab.off[j] = (j < nblk && e < E) ? p.offsets[e] : 0;
+    }
+  }
+  if constexpr (MODE == kStripChain) {
+    if (b == 0 && wave == 0) {
+#pragma unroll
+      for (int j = 0; j < kMaxBlocks; ++j) {
+        const int e = 64 * j + lane;
+        if (j < nblk && e < E) {
+          p.counts[e] = tab.cnt[j];
+          p.cursors[e] = tab.cnt[j];
+          p.offsets_out[e] = tab.off[j];
+        }
+      }
+      if (lane == 0) p.offsets_out[E] = seg_field(tab.off, E - 1) + seg_field(tab.cnt, E - 1);
+    }
+  }
+
+  const int total = tab.total_strips;
+  const int s0 = static_cast<int>(static_cast<long>(worker) * total / grid);
+  const int s1 = static_cast<int>(static_cast<long>(worker + 1) * total / grid);
+  StripInfo cur{};
+  if (s0 < s1) {
+    cur = strip_info(tab, nblk, E, s0);
+    if constexpr (MODE == kStripGrouped || MODE == kStripChain) load_b(cur.e);  // in flight below
+  }
+
+  // ------------------------------------------- chain: routes of my strips
+  float w_pending = 0.0F;
+  if constexpr (MODE == kStripChain) {
+    const int slots = (s1 - s0) * kRows;
+    for (int i = tid; i < slots; i += kThreads) s_slot[i] = -1;
+    // my segments (uniform): e, stable-rank window, slot of rank 0, row offset
+    int seg_e[kMaxSegs], seg_lo[kMaxSegs], seg_hi[kMaxSegs], seg_base[kMaxSegs], seg_off[kMaxSegs];
+    int nseg = 0;
+    for (int s = s0; s < s1 && nseg < kMaxSegs; ++nseg) {
+      const int e = seg_find(tab, nblk, E, s);
+      const int pre_e = seg_field(tab.pre, e);
+      const int rows_e = seg_field(tab.cnt, e);
+      const int end_e = pre_e + strips_of(rows_e);
+      const int last = s1 < end_e ? s1 : end_e;
+      const int hi = (last - pre_e) * kRows;
+      seg_e[nseg] = e;
+      seg_lo[nseg] = (s - pre_e) * kRows;
+      seg_hi[nseg] = hi < rows_e ? hi : rows_e;
+      seg_base[nseg] = (pre_e - s0) * kRows;
+      seg_off[nseg] = seg_field(tab.off, e);
+      s = last;
+    }
+    // pass 1: routes of each of my segments in this wave's chunks
+#pragma unroll
+    for (int i = 0; i < kMaxSegs; ++i) {
+      if (i < nseg) {
+        int32_t n = 0;
+#pragma unroll
+        for (int u = 0; u < kIdChunks; ++u) {
+          if (c_begin + u < c_end) {
+            n += __popcll(__ballot(idv[u].x == seg_e[i])) + __popcll(__ballot(idv[u].y == seg_e[i])) +
+                 __popcll(__ballot(idv[u].z == seg_e[i])) + __popcll(__ballot(idv[u].w == seg_e[i]));
+          }
+        }
+        if (lane == 0) s_misc[wave * kMaxSegs + i] = n;
+      }
+    }
+    __syncthreads();
+    // pass 2: stable ranks (route order = wave, chunk, lane, component); keep
+    // the ones that fall in my strips
+    const uint64_t lt = lanemask_lt();
+#pragma unroll
+    for (int i = 0; i < kMaxSegs; ++i) {
+      if (i < nseg) {
+        const int e = seg_e[i];
+        int32_t q = 0;
+        for (int w = 0; w < wave; ++w) q += s_misc[w * kMaxSegs + i];
+#pragma unroll
+        for (int u = 0; u < kIdChunks; ++u) {
+          if (c_begin + u < c_end && q < seg_hi[i]) {
+            const uint64_t m0 = __ballot(idv[u].x == e);
+            const uint64_t m1 = __ballot(idv[u].y == e);
+            const uint64_t m2 = __ballot(idv[u].z == e);
+            const uint64_t m3 = __ballot(idv[u].w == e);
+            int rank = q + __popcll(m0 & lt) + __popcll(m1 & lt) + __popcll(m2 & lt) +
+                       __popcll(m3 & lt);
+            const int r = (c_begin + u) * 256 + 4 * lane;
+            const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              if (vals[k] == e) {
+                if (rank >= seg_lo[i] && rank < seg_hi[i]) s_slot[seg_base[i] + rank] = r + k;
+                ++rank;
+              }
+            }
+            q += __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // route map entries of my rows; the route weights are loaded now and
+    // stored to LDS with the first strip's A rows
+    if (tid < slots) {  // slots <= kMaxSegs * 16 <= kThreads
+      const int32_t route = s_slot[tid];
+      if (route >= 0) {
+        int row = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxSegs; ++i) {
+          if (i < nseg && tid >= seg_base[i] + seg_lo[i] && tid < seg_base[i] + seg_hi[i]) {
+            row = seg_off[i] + (tid - seg_base[i]);
+          }
+        }
+        p.route_pos[route] = row;
+        if (p.sorted_route != nullptr) p.sorted_route[row] = route;
+        w_pending = p.route_weights[route];
+      }
+    }
+  }
+
+  // ------------------------------------------------------------ strip loop
+  // A staging: thread t loads row t / kRowThreads, float4 columns
+  // (t % kRowThreads) + kRowThreads u (row-contiguous across the threads).
+  const int a_row = tid / kRowThreads;
+  const int a_col = tid % kRowThreads;
+  auto a_source = [&](int s, const StripInfo& si) -> int {
+    if constexpr (MODE == kStripChain) {
+      (void)si;
+      const int32_t route = s_slot[(s - s0) * kRows + a_row];
+      return route >= 0 ? (route >> 1) : -1;  // top-2: route = 2 * token + rank
+    } else {
+      (void)s;
+      const int row = si.row0 + a_row;
+      return row < si.row_end ? row : -1;
+    }
+  };
+  v4f a_regs[kALoads];
+  auto load_a = [&](int src) {
+    const float* row = p.A + static_cast<std::size_t>(src < 0 ? 0 : src) * K;
+#pragma unroll
+    for (int u = 0; u < kALoads; ++u) {
+      const int k = 4 * (a_col + kRowThreads * u);
+      a_regs[u] = load_or_zero(row + (k < K ? k : K - 4), src >= 0 && k < K);
+    }
+  };
+
+  int cur_e = -1;
+  int src = -1;
+  if (s0 < s1) {
+    src = a_source(s0, cur);
+    load_a(src);
+  }
+  for (int s = s0; s < s1; ++s) {
+    const StripInfo si = cur;
+    __syncthreads();  // every wave is done with As (and with Bs, if it changes)
+    if (si.e != cur_e) {
+      store_b();  // breg holds B of si.e (loaded ahead)
+      cur_e = si.e;
+    }
+    // ---- this strip's A rows -> LDS (zeros past K up to the chunk edge) ----
+#pragma unroll
+    for (int u = 0; u < kALoads; ++u) {
+      const int k = 4 * (a_col + kRowThreads * u);
+      if (k < chunks * 16) *reinterpret_cast<v4f*>(As + a_row * kLd + k) = a_regs[u];
+    }
+    if constexpr (MODE == kStripChain) {
+      if (src >= 0) {  // gathered rows -> x_permuted
+        float* out = p.x_permuted + static_cast<std::size_t>(si.row0 + a_row) * K;
+#pragma unroll
+        for (int u = 0; u < kALoads; ++u) {
+          const int k = 4 * (a_col + kRowThreads * u);
+          if (k < K) *reinterpret_cast<v4f*>(out + k) = a_regs[u];
+        }
+      }
+      if (s == s0 && tid < (s1 - s0) * kRows) s_w[tid] = w_pending;
+    }
+    __syncthreads();
+    // ---- prefetch the next strip's A rows (and B of its segment) ----
+    if (s + 1 < s1) {
+      cur = strip_info(tab, nblk, E, s + 1);
+      src = a_source(s + 1, cur);
+      load_a(src);
+      if (cur.e != si.e) load_b(cur.e);
+    }
+
+    // ---- MFMA: acc = rows x columns [16 wave, 16 wave + 16) ----
+    v4f acc = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+    const float* aw = As + li * kLd + 4 * g;
+    const float* bw = Bs + (16 * wave + li) * kLd + 4 * g;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c < chunks) {
+        const v4f af = *reinterpret_cast<const v4f*>(aw + 16 * c);
+        const v4f bf = *reinterpret_cast<const v4f*>(bw + 16 * c);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
+      }
+    }
+
+    // ---- epilogue: acc[r] is row 4g + r, column 16 wave + li ----
+    const int col = 16 * wave + li;
+    if constexpr (MODE == kStripChain) {
+      const int slot0 = (s - s0) * kRows;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 4 * g + r;
+        const int32_t route = s_slot[slot0 + rl];
+        if (route < 0 || col >= N) continue;
+        const float w = s_w[slot0 + rl];
+        p.C[static_cast<std::size_t>(si.row0 + rl) * N + col] = acc[r];
+        // Both routes of a token add into the zeroed output: fl(0 + a) + b is
+        // the same in either order, so the combine is deterministic.
+        unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col, __fmul_rn(w, acc[r]));
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = si.row0 + 4 * g + r;
+        if (row < si.row_end && col < N) p.C[static_cast<std::size_t>(row) * N + col] = acc[r];
+      }
+    }
+    if constexpr (MODE == kStripRouterGate) {
+      // Top-2 of each row over its N logits: per wave over its 16 columns
+      // (the 16 lanes of a DPP row hold one output row), then over the waves
+      // through LDS.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = si.row0 + 4 * g + r;
+        uint64_t k1 = 0, k2 = 0;
+        if (row < si.row_end && col < N) k1 = rr::dev::gate_key(acc[r], col);
+        rr::dev::merge_top2_row16(k1, k2);
+        if (li == 0) {
+          s_keys[(wave * kRows + 4 * g + r) * 2] = k1;
+          s_keys[(wave * kRows + 4 * g + r) * 2 + 1] = k2;
+        }
+      }
+      __syncthreads();
+      const int rows = si.row_end - si.row0 < kRows ? si.row_end - si.row0 : kRows;
+      if (tid < rows) {
+        uint64_t k1 = 0, k2 = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          rr::dev::insert_key(s_keys[(w * kRows + tid) * 2], k1, k2);
+          rr::dev::insert_key(s_keys[(w * kRows + tid) * 2 + 1], k1, k2);
+        }
+        float w1, w2;
+        rr::dev::gate_weights(k1, k2, &w1, &w2);
+        const std::size_t row = static_cast<std::size_t>(si.row0 + tid);
+        p.gate_ids[2 * row] = rr::dev::key_expert(k1);
+        p.gate_ids[2 * row + 1] = rr::dev::key_expert(k2);
+        p.gate_weights[2 * row] = w1;
+        p.gate_weights[2 * row + 1] = w2;
+      }
+      if (p.y_zero != nullptr) {
+        float* base = p.y_zero + static_cast<std::size_t>(si.row0) * p.y_cols;
+        const int n = rows * p.y_cols;
+        if ((p.y_cols & 3) == 0 && (reinterpret_cast<std::uintptr_t>(p.y_zero) & 15u) == 0) {
+          for (int i = tid; i < n / 4; i += kThreads) {
+            reinterpret_cast<v4f*>(base)[i] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+          }
+        } else {
+          for (int i = tid; i < n; i += kThreads) base[i] = 0.0F;
+        }
+      }
+    }
+  }
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices] = {};
+
+int cu_count() {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 256;
+  if (device >= 0 && device < kMaxDevices) {
+    const int cached = g_cus[device].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0) {
+    cus = 256;
+  }
+  if (device >= 0 && device < kMaxDevices) g_cus[device].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+constexpr std::size_t kLdsLimit = 160 * 1024;  // gfx950 LDS per workgroup
+
+template <class Kernel>
+hipError_t allow_lds(Kernel kernel) {
+  static const hipError_t status = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(kLdsLimit));
+  return status;
+}
+
+int bn_for(int n) { return n <= 64 ? 64 : 128; }
+
+// Dynamic LDS bytes of one launch.
+std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
+  const int chunks = (K + 15) >> 4;
+  const std::size_t stage = static_cast<std::size_t>(bn + kRows) * (chunks * 16 + 4);
+  std::size_t bytes = stage * sizeof(float);
+  const int waves = bn / 16;
+  if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(waves) * kRows * 2 * sizeof(uint64_t);
+  (void)segments;
+  bytes += (kMaxBlocks * 64 + static_cast<std::size_t>(waves) * kMaxSegs) * sizeof(int32_t);
+  if (mode == kStripChain) bytes += 2 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);
+  return bytes;
+}
+
+template <int BN, int MODE, int CHUNKS>
+hipError_t launch_strip_3(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
+  const hipError_t attr = allow_lds(rr_strip_gemm_kernel<BN, MODE, CHUNKS>);
+  if (attr != hipSuccess) return attr;
+  rr_strip_gemm_kernel<BN, MODE, CHUNKS><<<grid, strip_threads<BN>(), lds, stream>>>(p);
+  return hipGetLastError();
+}
+
+template <int BN, int MODE>
+hipError_t launch_strip_2(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
+  return p.K == 256 ? launch_strip_3<BN, MODE, 16>(p, grid, lds, stream)
+                    : launch_strip_3<BN, MODE, 0>(p, grid, lds, stream);
+}
+
+template <int MODE>
+hipError_t launch_strip(const StripParams& p, int grid, hipStream_t stream) {
+  const int bn = bn_for(p.N);
+  const std::size_t lds = strip_lds(bn, MODE, p.K, p.segments, p.max_strips);
+  if (lds > kLdsLimit) return hipErrorInvalidValue;
+  if (grid < 1) grid = 1;
+  return bn == 64 ? launch_strip_2<64, MODE>(p, grid, lds, stream)
+                  : launch_strip_2<128, MODE>(p, grid, lds, stream);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+int grid_for(long strips_bound) {
+  const long cus = cu_count();
+  long grid = strips_bound < cus ? strips_bound : cus;
+  if (grid >= kXcds) grid = grid / kXcds * kXcds;
+  return static_cast<int>(grid < 1 ? 1 : grid);
+}
+
+StripParams base(const float* a, const float* w, float* c, int m, int k, int n, int segments) {
+  StripParams p{};
+  p.A = a;
+  p.W = w;
+  p.C = c;
+  p.M = m;
+  p.K = k;
+  p.N = n;
+  p.segments = segments;
+  return p;
+}
+
+}  // namespace
+
+bool strip_shape_ok(int k, int n, const void* a, const void* w) {
+  return k > 0 && k <= 256 && (k & 3) == 0 && n > 0 && n <= 128 && (n & 3) == 0 && aligned16(a) &&
+         aligned16(w);
+}
+
+bool strip_segments_ok(int segments) { return segments >= 1 && segments <= kMaxBlocks * 64; }
+
+bool strip_chain_ok(int tokens, int experts, int k, int n, const void* x, const void* w,
+                    const void* ids, const void* x_permuted) {
+  if (!strip_shape_ok(k, n, x, w) || !aligned16(ids) || !aligned16(x_permuted)) return false;
+  if (!strip_segments_ok(experts) || tokens <= 0 || tokens > 8192) return false;
+  const long routes = 2L * tokens;
+  const long bound = (routes + kRows - 1) / kRows + experts;
+  const int grid = grid_for(bound);
+  const int max_strips = static_cast<int>((bound + grid - 1) / grid);
+  // a workgroup's strips span at most max_strips segments
+  return max_strips <= kMaxSegs &&
+         strip_lds(bn_for(n), kStripChain, k, experts, max_strips) <= kLdsLimit;
+}
+
+hipError_t strip_dense(const float* a, const float* b, float* c, int m, int n, int k,
+                       hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  const StripParams p = base(a, b, c, m, k, n, 1);
+  return launch_strip<kStripDense>(p, grid_for((m + kRows - 1) / kRows), stream);
+}
+
+hipError_t strip_grouped(const float* x, const float* w, const int32_t* offsets, float* y,
+                         int experts, int hidden, int output, long rows_bound, hipStream_t stream) {
+  StripParams p = base(x, w, y, 0, hidden, output, experts);
+  p.offsets = offsets;
+  const long bound = (rows_bound + kRows - 1) / kRows + experts;
+  return launch_strip<kStripGrouped>(p, grid_for(bound), stream);
+}
+
+hipError_t strip_router_gate(const float* x, const float* router_weights, float* logits,
+                             int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
+                             int tokens, int experts, int hidden, hipStream_t stream) {
+  if (tokens <= 0) return hipSuccess;
+  StripParams p = base(x, router_weights, logits, tokens, hidden, experts, 1);
+  p.gate_ids = ids;
+  p.gate_weights = gate_weights;
+  p.y_zero = y_zero;
+  p.y_cols = y_cols;
+  return launch_strip<kStripRouterGate>(p, grid_for((tokens + kRows - 1) / kRows), stream);
+}
+
+hipError_t strip_chain(const float* x, const float* expert_weights, const int32_t* ids,
+                       const float* route_weights, int32_t* counts, int32_t* offsets,
+                       int32_t* cursors, int32_t* route_pos, int32_t* sorted_route,
+                       float* x_permuted, float* y_permuted, float* y, int tokens, int experts,
+                       int hidden, int output, hipStream_t stream) {
+  if (tokens <= 0) return hipSuccess;
+  const int routes = 2 * tokens;
+  StripParams p = base(x, expert_weights, y_permuted, routes, hidden, output, experts);
+  const long bound = (static_cast<long>(routes) + kRows - 1) / kRows + experts;
+  const int grid = grid_for(bound);
+  p.max_strips = static_cast<int>((bound + grid - 1) / grid);
+  p.ids = ids;
+  p.route_weights = route_weights;
+  p.counts = counts;
+  p.offsets_out = offsets;
+  p.cursors = cursors;
+  p.route_pos = route_pos;
+  p.sorted_route = sorted_route;
+  p.x_permuted = x_permuted;
+  p.y = y;
+  if (p.max_strips > kMaxSegs) return hipErrorInvalidValue;  // strip_chain_ok excludes it
+  return launch_strip<kStripChain>(p, grid, stream);
+}
+
+}  // namespace rr::kern

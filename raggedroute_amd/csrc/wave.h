@@ -33,15 +33,32 @@ __host__ __device__ __forceinline__ int bits_for(int experts) {
   return bits;
 }
 
-// Inclusive wave scan of int32 values (wraps like the reference's int32 sums).
-__device__ __forceinline__ int32_t wave_inclusive_scan(int32_t x) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int32_t y = __shfl_up(x, d, kWave);
-    if (lane >= d) x = static_cast<int32_t>(static_cast<uint32_t>(x) + static_cast<uint32_t>(y));
-  }
-  return x;
+// DPP lane moves (gfx9 encodings). A lane whose source is out of range, or
+// whose row is masked off, receives 0.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xf, false));
+}
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row -> the next row
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 -> rows 2 and 3
+
+// Inclusive wave scan of int32 values (wraps like the reference's int32 sums):
+// shifts of 1, 2, 4, 8 inside rows of 16 lanes, then the row totals are
+// carried across rows. Register-to-register moves, no LDS round trips.
+__device__ __forceinline__ int32_t wave_inclusive_scan(int32_t v) {
+  uint32_t x = static_cast<uint32_t>(v);
+  x += dpp_move<kDppRowShr1>(x);
+  x += dpp_move<kDppRowShr2>(x);
+  x += dpp_move<kDppRowShr4>(x);
+  x += dpp_move<kDppRowShr8>(x);
+  x += dpp_move<kDppRowBcast15, 0xa>(x);
+  x += dpp_move<kDppRowBcast31, 0xc>(x);
+  return static_cast<int32_t>(x);
 }
 
 }  // namespace rr::dev

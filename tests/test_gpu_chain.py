@@ -252,3 +252,32 @@ def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):
         assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
                               b.view(np.uint32) if b.dtype == np.float32 else b), f"{key} differs"
     check_chain(cfg, inp, fused)
+
+
+@pytest.mark.parametrize("kind,hidden", [("tokens", 48), ("logits", 48), ("tokens", 260), ("logits", 260)])
+def test_fused_launches_one_by_one_equal_chain(ctx, device, kind, hidden):
+    """rr_chain_fused_launch over every launch in order writes what one chain
+    call writes (merged route prep for K <= 256, separate above); an index past
+    the last launch is rejected."""
+    cfg = workloads.ChainConfig("hook", 300, 16, hidden, 40, from_tokens=kind == "tokens")
+    inp = workloads.chain_inputs(cfg, seed=11)
+    whole = ChainRun(cfg, inp, device).run(ctx)
+    run = ChainRun(cfg, inp, device)
+    c = rr.RuntimeContext(stream=ctx.stream, workspace=run.ws.data_ptr(),
+                          workspace_bytes=run.ws.numel() * 4, architecture=ctx.architecture)
+    names = rr.chain_fused_launch_names(run.args, cfg.from_tokens)
+    assert names[0] == ("router_gate" if kind == "tokens" else "gate") and len(names) in (2, 3)
+    for index in range(len(names)):
+        status = rr.chain_fused_launch(run.args, c, cfg.from_tokens, index)
+        assert status.ok(), status.message
+    torch.cuda.synchronize()
+    status = rr.chain_fused_launch(run.args, c, cfg.from_tokens, len(names))
+    assert status.code == rr.StatusCode.kInvalidArgument
+    parts = {name: to_host(getattr(run, attr)) for name, attr in
+             [("logits", "logits"), ("ids", "ids"), ("weights", "w"), ("counts", "counts"),
+              ("offsets", "offsets"), ("route_pos", "pos"), ("y", "y"), ("x_permuted", "xp"),
+              ("y_permuted", "yp"), ("sorted_route", "inv")]}
+    for key, a in parts.items():
+        b = whole[key]
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), f"{key} differs"
