@@ -140,6 +140,7 @@ __device__ __forceinline__ int32_t seg_field(const int32_t (&col)[kMaxBlocks], i
 
 // Segment of strip s: the last segment whose first strip is <= s (it is never
 // empty, since an empty segment shares its first strip with the next one).
+// Every lane of the wave must be active (ballot).
 __device__ __forceinline__ int seg_find(const SegTable& t, int nblk, int segments, int s) {
   const int lane = lane_id();
 #pragma unroll
@@ -337,84 +338,94 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
   if constexpr (MODE == kStripChain) {
     const int slots = (s1 - s0) * kRows;
     for (int i = tid; i < slots; i += kThreads) s_slot[i] = -1;
-    // my segments (uniform): e, stable-rank window, slot of rank 0, row offset
-    int seg_e[kMaxSegs], seg_lo[kMaxSegs], seg_hi[kMaxSegs], seg_base[kMaxSegs], seg_off[kMaxSegs];
-    int nseg = 0;
-    for (int s = s0; s < s1 && nseg < kMaxSegs; ++nseg) {
-      const int e = seg_find(tab, nblk, E, s);
-      const int pre_e = seg_field(tab.pre, e);
-      const int rows_e = seg_field(tab.cnt, e);
+    // My segments, walked again in each pass (uniform values; runtime loops
+    // keep one copy of the unrolled chunk code): segment e covers my strips
+    // [s, last), i.e. its stable ranks [lo, hi), stored from slot base + rank.
+    struct Seg {
+      int e, lo, hi, base, off, last;
+    };
+    // Called in uniform control flow only (seg_find ballots over the wave).
+    auto seg_at = [&](int s) -> Seg {
+      Seg sg;
+      sg.e = seg_find(tab, nblk, E, s);
+      const int pre_e = seg_field(tab.pre, sg.e);
+      const int rows_e = seg_field(tab.cnt, sg.e);
       const int end_e = pre_e + strips_of(rows_e);
-      const int last = s1 < end_e ? s1 : end_e;
-      const int hi = (last - pre_e) * kRows;
-      seg_e[nseg] = e;
-      seg_lo[nseg] = (s - pre_e) * kRows;
-      seg_hi[nseg] = hi < rows_e ? hi : rows_e;
-      seg_base[nseg] = (pre_e - s0) * kRows;
-      seg_off[nseg] = seg_field(tab.off, e);
-      s = last;
-    }
+      sg.last = s1 < end_e ? s1 : end_e;
+      const int hi = (sg.last - pre_e) * kRows;
+      sg.lo = (s - pre_e) * kRows;
+      sg.hi = hi < rows_e ? hi : rows_e;
+      sg.base = (pre_e - s0) * kRows;
+      sg.off = seg_field(tab.off, sg.e);
+      return sg;
+    };
     // pass 1: routes of each of my segments in this wave's chunks
-#pragma unroll
-    for (int i = 0; i < kMaxSegs; ++i) {
-      if (i < nseg) {
+    {
+      int i = 0;
+#pragma unroll 1
+      for (int s = s0; s < s1 && i < kMaxSegs; ++i) {
+        const Seg sg = seg_at(s);
         int32_t n = 0;
 #pragma unroll
         for (int u = 0; u < kIdChunks; ++u) {
           if (c_begin + u < c_end) {
-            n += __popcll(__ballot(idv[u].x == seg_e[i])) + __popcll(__ballot(idv[u].y == seg_e[i])) +
-                 __popcll(__ballot(idv[u].z == seg_e[i])) + __popcll(__ballot(idv[u].w == seg_e[i]));
+            n += __popcll(__ballot(idv[u].x == sg.e)) + __popcll(__ballot(idv[u].y == sg.e)) +
+                 __popcll(__ballot(idv[u].z == sg.e)) + __popcll(__ballot(idv[u].w == sg.e));
           }
         }
         if (lane == 0) s_misc[wave * kMaxSegs + i] = n;
+        s = sg.last > s ? sg.last : s1;  // always advances
       }
     }
     __syncthreads();
     // pass 2: stable ranks (route order = wave, chunk, lane, component); keep
     // the ones that fall in my strips
-    const uint64_t lt = lanemask_lt();
-#pragma unroll
-    for (int i = 0; i < kMaxSegs; ++i) {
-      if (i < nseg) {
-        const int e = seg_e[i];
+    {
+      const uint64_t lt = lanemask_lt();
+      int i = 0;
+#pragma unroll 1
+      for (int s = s0; s < s1 && i < kMaxSegs; ++i) {
+        const Seg sg = seg_at(s);
         int32_t q = 0;
         for (int w = 0; w < wave; ++w) q += s_misc[w * kMaxSegs + i];
 #pragma unroll
         for (int u = 0; u < kIdChunks; ++u) {
-          if (c_begin + u < c_end && q < seg_hi[i]) {
-            const uint64_t m0 = __ballot(idv[u].x == e);
-            const uint64_t m1 = __ballot(idv[u].y == e);
-            const uint64_t m2 = __ballot(idv[u].z == e);
-            const uint64_t m3 = __ballot(idv[u].w == e);
+          if (c_begin + u < c_end && q < sg.hi) {
+            const uint64_t m0 = __ballot(idv[u].x == sg.e);
+            const uint64_t m1 = __ballot(idv[u].y == sg.e);
+            const uint64_t m2 = __ballot(idv[u].z == sg.e);
+            const uint64_t m3 = __ballot(idv[u].w == sg.e);
             int rank = q + __popcll(m0 & lt) + __popcll(m1 & lt) + __popcll(m2 & lt) +
                        __popcll(m3 & lt);
             const int r = (c_begin + u) * 256 + 4 * lane;
             const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              if (vals[k] == e) {
-                if (rank >= seg_lo[i] && rank < seg_hi[i]) s_slot[seg_base[i] + rank] = r + k;
+              if (vals[k] == sg.e) {
+                if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = r + k;
                 ++rank;
               }
             }
             q += __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
           }
         }
+        s = sg.last > s ? sg.last : s1;  // always advances
       }
     }
     __syncthreads();
     // route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows
+    // (the walk runs in uniform control flow: seg_find's ballot needs every lane)
+    int row = 0;
+#pragma unroll 1
+    for (int s = s0; s < s1;) {
+      const Seg sg = seg_at(s);
+      if (tid >= sg.base + sg.lo && tid < sg.base + sg.hi) row = sg.off + (tid - sg.base);
+      s = sg.last > s ? sg.last : s1;
+    }
     if (tid < slots) {  // slots <= kMaxSegs * 16 <= kThreads
       const int32_t route = s_slot[tid];
       if (route >= 0) {
-        int row = 0;
-#pragma unroll
-        for (int i = 0; i < kMaxSegs; ++i) {
-          if (i < nseg && tid >= seg_base[i] + seg_lo[i] && tid < seg_base[i] + seg_hi[i]) {
-            row = seg_off[i] + (tid - seg_base[i]);
-          }
-        }
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
         w_pending = p.route_weights[route];
