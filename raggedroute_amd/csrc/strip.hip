@@ -153,6 +153,76 @@ __device__ __forceinline__ int seg_find(const SegTable& t, int nblk, int segment
   return 0;
 }
 
+// Sum over the wave of a per-lane value (every lane active).
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+  return __builtin_amdgcn_readlane(rr::dev::wave_inclusive_scan(v), 63);
+}
+
+struct StripRange {
+  int s0, s1;
+};
+
+// Strips [s0, s1) of one worker. Preferred: segment-aligned ranges, m strips
+// per worker with ceil(strips_e / m) workers per segment, so a worker loads
+// one segment's B once. m is the smallest value for which those workers fit
+// the grid; when that costs more than one strip over the even split (many
+// small segments), or exceeds cap, the strips are split evenly in contiguous
+// ranges that may span segments.
+__device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk, int segments,
+                                                    int total, int grid, int worker, int cap) {
+  const int lane = lane_id();
+  const int m_even = (total + grid - 1) / grid;
+  int m = m_even > 0 ? m_even : 1;
+  int need = 0;
+  for (int it = 0; it < 2; ++it, ++m) {
+    need = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      if (j < nblk) need += wave_sum((strips_of(t.cnt[j]) + m - 1) / m);
+    }
+    if (need <= grid) break;
+  }
+  StripRange r;
+  if (need <= grid && m <= cap) {
+    // workers of segment e: [wpre_e, wpre_e + ceil(strips_e / m))
+    int32_t wpre[kMaxBlocks];
+    int32_t carry = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      if (j < nblk) {
+        const int32_t wk = (strips_of(t.cnt[j]) + m - 1) / m;
+        const int32_t incl = rr::dev::wave_inclusive_scan(wk);
+        wpre[j] = carry + incl - wk;
+        carry += __builtin_amdgcn_readlane(incl, 63);
+      } else {
+        wpre[j] = INT_MAX;
+      }
+    }
+    r.s0 = r.s1 = 0;
+    if (worker < carry) {
+      int e = 0;
+#pragma unroll
+      for (int j = kMaxBlocks - 1; j >= 0; --j) {
+        const uint64_t mask = __ballot(64 * j + lane < segments && wpre[j] <= worker);
+        if (mask != 0) {
+          e = 64 * j + 63 - __builtin_clzll(mask);
+          break;
+        }
+      }
+      const int first = seg_field(wpre, e);
+      const int pre_e = seg_field(t.pre, e);
+      const int end_e = pre_e + strips_of(seg_field(t.cnt, e));
+      r.s0 = pre_e + (worker - first) * m;
+      r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
+      if (r.s0 > r.s1) r.s0 = r.s1;
+    }
+  } else {
+    r.s0 = static_cast<int>(static_cast<long>(worker) * total / grid);
+    r.s1 = static_cast<int>(static_cast<long>(worker + 1) * total / grid);
+  }
+  return r;
+}
+
 struct StripInfo {
   int e;        // segment
   int row0;     // first row of the strip (segment order)
@@ -325,12 +395,17 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
   }
 
   const int total = tab.total_strips;
-  const int s0 = static_cast<int>(static_cast<long>(worker) * total / grid);
-  const int s1 = static_cast<int>(static_cast<long>(worker + 1) * total / grid);
+  int s0, s1;
+  {
+    const StripRange range = assign_strips(tab, nblk, E, total, grid, worker,
+                                           MODE == kStripChain ? p.max_strips : INT_MAX);
+    s0 = range.s0;
+    s1 = range.s1;
+  }
   StripInfo cur{};
   if (s0 < s1) {
     cur = strip_info(tab, nblk, E, s0);
-    if constexpr (MODE == kStripGrouped || MODE == kStripChain) load_b(cur.e);  // in flight below
+    if constexpr (MODE == kStripGrouped) load_b(cur.e);  // in flight below
   }
 
   // ------------------------------------------- chain: routes of my strips
@@ -413,6 +488,10 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       }
     }
     __syncthreads();
+    // B of the first segment: issued after the rank passes, whose waves would
+    // otherwise stall behind the 16 loads each, and in flight with the route
+    // map below.
+    if (s0 < s1) load_b(cur.e);
     // route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows
     // (the walk runs in uniform control flow: seg_find's ballot needs every lane)
@@ -423,7 +502,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       if (tid >= sg.base + sg.lo && tid < sg.base + sg.hi) row = sg.off + (tid - sg.base);
       s = sg.last > s ? sg.last : s1;
     }
-    if (tid < slots) {  // slots <= kMaxSegs * 16 <= kThreads
+    if (tid < slots) {  // slots <= (kMaxSegs + 1) * 16 <= kThreads
       const int32_t route = s_slot[tid];
       if (route >= 0) {
         p.route_pos[route] = row;
@@ -688,9 +767,10 @@ bool strip_chain_ok(int tokens, int experts, int k, int n, const void* x, const 
   const long routes = 2L * tokens;
   const long bound = (routes + kRows - 1) / kRows + experts;
   const int grid = grid_for(bound);
-  const int max_strips = static_cast<int>((bound + grid - 1) / grid);
-  // a workgroup's strips span at most max_strips segments
-  return max_strips <= kMaxSegs &&
+  // strips per workgroup: up to ceil(bound / grid) in even contiguous ranges
+  // (spanning at most that many segments), one more in segment-aligned ones
+  const int max_strips = static_cast<int>((bound + grid - 1) / grid) + 1;
+  return max_strips <= kMaxSegs + 1 &&
          strip_lds(bn_for(n), kStripChain, k, experts, max_strips) <= kLdsLimit;
 }
 
@@ -731,7 +811,7 @@ hipError_t strip_chain(const float* x, const float* expert_weights, const int32_
   StripParams p = base(x, expert_weights, y_permuted, routes, hidden, output, experts);
   const long bound = (static_cast<long>(routes) + kRows - 1) / kRows + experts;
   const int grid = grid_for(bound);
-  p.max_strips = static_cast<int>((bound + grid - 1) / grid);
+  p.max_strips = static_cast<int>((bound + grid - 1) / grid) + 1;
   p.ids = ids;
   p.route_weights = route_weights;
   p.counts = counts;
@@ -741,7 +821,7 @@ hipError_t strip_chain(const float* x, const float* expert_weights, const int32_
   p.sorted_route = sorted_route;
   p.x_permuted = x_permuted;
   p.y = y;
-  if (p.max_strips > kMaxSegs) return hipErrorInvalidValue;  // strip_chain_ok excludes it
+  if (p.max_strips > kMaxSegs + 1) return hipErrorInvalidValue;  // strip_chain_ok excludes it
   return launch_strip<kStripChain>(p, grid, stream);
 }
 
