@@ -351,7 +351,7 @@ def profile(torch, device, case):
         for _ in range(5):
             ch.chain()
         torch.cuda.synchronize()
-        for index in range(3):
+        for index in range(len(ch.rr.chain_fused_launch_names(ch.chain_args, cfg.from_tokens))):
             for _ in range(3):
                 ch.fused_launch(index)
         for name in ch.stage_args:

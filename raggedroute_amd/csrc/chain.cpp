@@ -92,7 +92,11 @@ rr_status run_fused(const rr_chain_args* a, const rr_runtime_context& ctx, bool 
   const bool merged = merged_prep(a);
   hipError_t err = hipSuccess;
   if (only < 0 || only == 0) {
-    if (from_tokens && a->experts <= 128) {
+    // The router GEMM carries the gate in its epilogue where the strip kernel
+    // covers it (K <= 256, E <= 128); longer K runs the tiled dense GEMM (its
+    // best tiles need no epilogue staging) and the gate kernel.
+    if (from_tokens && a->experts <= 128 &&
+        kern::strip_shape_ok(a->hidden, a->experts, a->x, a->router_weights)) {
       err = kern::router_gate_mfma(a->x, a->router_weights, a->logits, a->expert_ids,
                                    a->route_weights, a->y, a->output, a->tokens, a->experts,
                                    a->hidden, ctx.stream);

@@ -2,7 +2,9 @@
 //
 // One persistent kernel serves the router dense GEMM (one segment of M rows),
 // the ragged grouped GEMM (segments [offsets[e], offsets[e+1]) with weights
-// W[e]) and the two fused forms used by the chain entries. The host never
+// W[e]) and the chain's gathered expert GEMM with the unpermute in its
+// epilogue, for shapes the narrow-output strip kernel (strip.hip) does not
+// cover. The host never
 // reads offsets: every workgroup loads them to LDS, builds the per-expert
 // row-tile prefix and walks the tile space (row tiles of every expert x column
 // tiles) with a grid-stride loop.
@@ -25,7 +27,6 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "gate.h"
 #include "launchers.h"
 #include "raggedroute_capi.h"
 #include "wave.h"
@@ -43,7 +44,6 @@ enum Mode : int {
   kGrouped = 1,       // segments from offsets, weights W[e]
   kChainGrouped = 2,  // grouped with A rows gathered through sorted_route, x_permuted
                       // written, and the top-2 unpermute folded into the epilogue
-  kRouterGate = 3,    // dense with the top-2 gate in the epilogue (needs N <= BN)
 };
 
 struct GemmParams {
@@ -61,12 +61,6 @@ struct GemmParams {
   const float* route_weights;
   float* x_permuted;
   float* y_out;
-  // kRouterGate: top-2 ids / weights of every row over its N logits, and the
-  // rows' [y_cols]-wide slice of y_zero zeroed for the chain's accumulation.
-  int32_t* gate_ids;
-  float* gate_weights;
-  float* y_zero;
-  int y_cols;
 };
 
 template <int BM_, int BN_, int WM_, int WN_, int BK_>
@@ -353,80 +347,31 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
       __syncthreads();
     }
 
-    if constexpr (MODE == kRouterGate) {
-      // Logit tile -> LDS (stage memory is free after the final barrier), then
-      // the logits are stored row-contiguous and every row's top-2 is taken by
-      // 16 lanes over its N columns.
-      constexpr int kLdT = S::BN + 1;
-      static_assert(S::BM * kLdT <= S::kStageFloats, "logit tile exceeds the stage");
-      float* tile = stages;
+    // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
 #pragma unroll
-      for (int i = 0; i < S::kTM; ++i)
+    for (int i = 0; i < S::kTM; ++i) {
 #pragma unroll
-        for (int j = 0; j < S::kTN; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            tile[(wm0 + i * 16 + 4 * g + r) * kLdT + wn0 + j * 16 + li] = acc[i][j][r];
-      __syncthreads();
-      const int rows = row_end - row0 < S::BM ? row_end - row0 : S::BM;
-      for (int idx = tid; idx < rows * N; idx += S::kThreads) {
-        const int r = idx / N;
-        const int c = idx - r * N;
-        prm.Y[static_cast<std::size_t>(row0 + r) * N + c] = tile[r * kLdT + c];
-      }
-      constexpr int kRowsPerPass = S::kThreads / 16;
-      for (int r0 = 0; r0 < S::BM; r0 += kRowsPerPass) {
-        const int r = r0 + tid / 16;
-        const int sub = tid & 15;
-        uint64_t k1 = 0, k2 = 0;
-        if (r < rows) {
-          for (int c = sub; c < N; c += 16) {
-            rr::dev::insert_key(rr::dev::gate_key(tile[r * kLdT + c], c), k1, k2);
-          }
+      for (int r = 0; r < 4; ++r) {
+        const int rl = wm0 + i * 16 + 4 * g + r;
+        const int row = row0 + rl;
+        if (row >= row_end) continue;
+        float* yrow = prm.Y + static_cast<std::size_t>(row) * N;
+        float* comb = nullptr;
+        float w = 0.0F;
+        if constexpr (MODE == kChainGrouped) {
+          comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
+          w = s_w[rl];
         }
-        rr::dev::merge_top2<16>(k1, k2);
-        if (sub == 0 && r < rows) {
-          float w1, w2;
-          rr::dev::gate_weights(k1, k2, &w1, &w2);
-          const std::size_t row = static_cast<std::size_t>(row0 + r);
-          prm.gate_ids[2 * row] = rr::dev::key_expert(k1);
-          prm.gate_ids[2 * row + 1] = rr::dev::key_expert(k2);
-          prm.gate_weights[2 * row] = w1;
-          prm.gate_weights[2 * row + 1] = w2;
-        }
-      }
-      if (prm.y_zero != nullptr) {
-        float* base = prm.y_zero + static_cast<std::size_t>(row0) * prm.y_cols;
-        for (long i = tid; i < static_cast<long>(rows) * prm.y_cols; i += S::kThreads) base[i] = 0.0F;
-      }
-      __syncthreads();  // the next tile's prologue reuses the stage memory
-    } else {
-      // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
 #pragma unroll
-      for (int i = 0; i < S::kTM; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int rl = wm0 + i * 16 + 4 * g + r;
-          const int row = row0 + rl;
-          if (row >= row_end) continue;
-          float* yrow = prm.Y + static_cast<std::size_t>(row) * N;
-          float* comb = nullptr;
-          float w = 0.0F;
-          if constexpr (MODE == kChainGrouped) {
-            comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
-            w = s_w[rl];
-          }
-#pragma unroll
-          for (int j = 0; j < S::kTN; ++j) {
-            const int col = n0 + wn0 + j * 16 + li;
-            if (col < N) {
-              yrow[col] = acc[i][j][r];
-              if constexpr (MODE == kChainGrouped) {
-                // Both routes of a token add into the zeroed output: fl(0 + a) + b
-                // is the same in either order, so the combine is deterministic
-                // and equals the rank-order unpermute.
-                unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
-              }
+        for (int j = 0; j < S::kTN; ++j) {
+          const int col = n0 + wn0 + j * 16 + li;
+          if (col < N) {
+            yrow[col] = acc[i][j][r];
+            if constexpr (MODE == kChainGrouped) {
+              // Both routes of a token add into the zeroed output: fl(0 + a) + b
+              // is the same in either order, so the combine is deterministic
+              // and equals the rank-order unpermute.
+              unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
             }
           }
         }
@@ -497,8 +442,6 @@ using TileSmall = TileShape<64, 64, 2, 2, 64>;
 using TileMedium = TileShape<32, 64, 2, 2, 64>;
 // 16x64, four 16x16 waves side by side, BK 64: narrow router GEMMs (N = E <= 64).
 using TileNarrow = TileShape<16, 64, 1, 4, 64>;
-// 16x128, four 16x32 waves side by side, BK 64: router GEMMs with 64 < E <= 128.
-using TileNarrowWide = TileShape<16, 128, 1, 4, 64>;
 
 // Whole-K tiles (K <= 256): one LDS stage holds all of K.
 using TileSmallK256 = TileShape<64, 64, 2, 2, 256>;    // 133 KB LDS
@@ -539,7 +482,7 @@ long tile_estimate(long rows, int segments, int bm, int n, int bn) {
 
 template <class S, int MODE>
 hipError_t launch_tile(const GemmParams& prm, long rows_per_expert, hipStream_t stream) {
-  const int segments = MODE == kDense || MODE == kRouterGate ? 1 : prm.experts;
+  const int segments = MODE == kDense ? 1 : prm.experts;
   return launch_gemm<S, MODE>(prm, tile_bound(segments, rows_per_expert, S::BM, prm.N, S::BN),
                               stream);
 }
@@ -613,18 +556,11 @@ hipError_t router_gate_mfma(const float* x, const float* router_weights, float* 
                             int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
                             int tokens, int experts, int hidden, hipStream_t stream) {
   if (tokens <= 0) return hipSuccess;
-  if (experts > 128) return hipErrorInvalidValue;
-  if (tile_override() == 0 && strip_shape_ok(hidden, experts, x, router_weights)) {
-    return strip_router_gate(x, router_weights, logits, ids, gate_weights, y_zero, y_cols, tokens,
-                             experts, hidden, stream);
-  }
-  GemmParams p = base_params(x, router_weights, nullptr, logits, 1, tokens, hidden, experts);
-  p.gate_ids = ids;
-  p.gate_weights = gate_weights;
-  p.y_zero = y_zero;
-  p.y_cols = y_cols;
-  if (experts <= 64) return launch_tile<TileNarrow, kRouterGate>(p, tokens, stream);
-  return launch_tile<TileNarrowWide, kRouterGate>(p, tokens, stream);
+  // The strip kernel carries the gate epilogue (E <= 128, K <= 256); callers
+  // run the dense GEMM and the gate kernel for other shapes.
+  if (experts > 128 || !strip_shape_ok(hidden, experts, x, router_weights)) return hipErrorInvalidValue;
+  return strip_router_gate(x, router_weights, logits, ids, gate_weights, y_zero, y_cols, tokens,
+                           experts, hidden, stream);
 }
 
 hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const int32_t* offsets,

@@ -20,7 +20,8 @@ hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offs
 
 // ---- fused chain forms (gemm.hip) ----
 // logits = x * router_weights with each row's top-2 ids / weights taken in the
-// epilogue; rows [0, tokens) of y_zero ([tokens, y_cols]) are zeroed. E <= 128.
+// epilogue; rows [0, tokens) of y_zero ([tokens, y_cols]) are zeroed. Strip
+// shapes only (E <= 128, K <= 256); hipErrorInvalidValue otherwise.
 hipError_t router_gate_mfma(const float* x, const float* router_weights, float* logits,
                             int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
                             int tokens, int experts, int hidden, hipStream_t stream);
