@@ -162,63 +162,78 @@ struct StripRange {
   int s0, s1;
 };
 
+// ceil(x / m) in 32-bit unsigned arithmetic (x >= 0, m >= 1).
+__device__ __forceinline__ int32_t ceil_div32(int32_t x, int32_t m) {
+  return static_cast<int32_t>((static_cast<uint32_t>(x) + static_cast<uint32_t>(m) - 1u) /
+                              static_cast<uint32_t>(m));
+}
+
+// Even contiguous split of [0, total) over grid workers: sizes q or q + 1
+// (no product of worker and total, so no overflow for any int32 total).
+__device__ __forceinline__ StripRange even_range(int total, int grid, int worker) {
+  const int q = total / grid;
+  const int rem = total - q * grid;
+  StripRange r;
+  r.s0 = worker * q + (worker < rem ? worker : rem);
+  r.s1 = r.s0 + q + (worker < rem ? 1 : 0);
+  return r;
+}
+
 // Strips [s0, s1) of one worker. Preferred: segment-aligned ranges, m strips
 // per worker with ceil(strips_e / m) workers per segment, so a worker loads
-// one segment's B once. m is the smallest value for which those workers fit
-// the grid; when that costs more than one strip over the even split (many
-// small segments), or exceeds cap, the strips are split evenly in contiguous
-// ranges that may span segments.
+// one segment's B once. m is the smallest of m_even = ceil(total / grid) and
+// m_even + 1 for which those workers fit the grid; otherwise (many small
+// segments), or when m exceeds cap, the even contiguous split is used.
 __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk, int segments,
                                                     int total, int grid, int worker, int cap) {
   const int lane = lane_id();
-  const int m_even = (total + grid - 1) / grid;
-  int m = m_even > 0 ? m_even : 1;
-  int need = 0;
-  for (int it = 0; it < 2; ++it, ++m) {
-    need = 0;
+  const int m0 = total > 0 ? (total + grid - 1) / grid : 1;
+  const int m1 = m0 + 1;
+  int32_t need0 = 0, need1 = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxBlocks; ++j) {
-      if (j < nblk) need += wave_sum((strips_of(t.cnt[j]) + m - 1) / m);
+  for (int j = 0; j < kMaxBlocks; ++j) {
+    if (j < nblk) {
+      const int32_t st = strips_of(t.cnt[j]);
+      need0 += wave_sum(ceil_div32(st, m0));
+      need1 += wave_sum(ceil_div32(st, m1));
     }
-    if (need <= grid) break;
+  }
+  const bool fit0 = need0 <= grid && m0 <= cap;
+  const bool fit1 = need1 <= grid && m1 <= cap;
+  if (!fit0 && !fit1) return even_range(total, grid, worker);
+  const int m = fit0 ? m0 : m1;
+  // workers of segment e: [wpre_e, wpre_e + ceil(strips_e / m))
+  int32_t wpre[kMaxBlocks];
+  int32_t carry = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxBlocks; ++j) {
+    if (j < nblk) {
+      const int32_t wk = ceil_div32(strips_of(t.cnt[j]), m);
+      const int32_t incl = rr::dev::wave_inclusive_scan(wk);
+      wpre[j] = carry + incl - wk;
+      carry += __builtin_amdgcn_readlane(incl, 63);
+    } else {
+      wpre[j] = INT_MAX;
+    }
   }
   StripRange r;
-  if (need <= grid && m <= cap) {
-    // workers of segment e: [wpre_e, wpre_e + ceil(strips_e / m))
-    int32_t wpre[kMaxBlocks];
-    int32_t carry = 0;
+  r.s0 = r.s1 = 0;
+  if (worker < carry) {
+    int e = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxBlocks; ++j) {
-      if (j < nblk) {
-        const int32_t wk = (strips_of(t.cnt[j]) + m - 1) / m;
-        const int32_t incl = rr::dev::wave_inclusive_scan(wk);
-        wpre[j] = carry + incl - wk;
-        carry += __builtin_amdgcn_readlane(incl, 63);
-      } else {
-        wpre[j] = INT_MAX;
+    for (int j = kMaxBlocks - 1; j >= 0; --j) {
+      const uint64_t mask = __ballot(64 * j + lane < segments && wpre[j] <= worker);
+      if (mask != 0) {
+        e = 64 * j + 63 - __builtin_clzll(mask);
+        break;
       }
     }
-    r.s0 = r.s1 = 0;
-    if (worker < carry) {
-      int e = 0;
-#pragma unroll
-      for (int j = kMaxBlocks - 1; j >= 0; --j) {
-        const uint64_t mask = __ballot(64 * j + lane < segments && wpre[j] <= worker);
-        if (mask != 0) {
-          e = 64 * j + 63 - __builtin_clzll(mask);
-          break;
-        }
-      }
-      const int first = seg_field(wpre, e);
-      const int pre_e = seg_field(t.pre, e);
-      const int end_e = pre_e + strips_of(seg_field(t.cnt, e));
-      r.s0 = pre_e + (worker - first) * m;
-      r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
-      if (r.s0 > r.s1) r.s0 = r.s1;
-    }
-  } else {
-    r.s0 = static_cast<int>(static_cast<long>(worker) * total / grid);
-    r.s1 = static_cast<int>(static_cast<long>(worker + 1) * total / grid);
+    const int first = seg_field(wpre, e);
+    const int pre_e = seg_field(t.pre, e);
+    const int end_e = pre_e + strips_of(seg_field(t.cnt, e));
+    r.s0 = pre_e + (worker - first) * m;
+    r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
+    if (r.s0 > r.s1) r.s0 = r.s1;
   }
   return r;
 }
@@ -254,6 +269,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
   constexpr int kRowThreads = kThreads / kRows;        // A staging: threads per row
   constexpr int kALoads = 64 / kRowThreads;            // float4 per thread (K <= 256)
   static_assert(BN == 64 || BN == 128, "BN is 64 or 128");
+  constexpr bool kSingle = MODE == kStripDense || MODE == kStripRouterGate;  // one segment
   extern __shared__ __align__(16) float lds[];
 
   const int K = p.K;
@@ -365,11 +381,12 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       const int32_t hi = p.offsets[ec + 1];
       tab.cnt[j] = (j < nblk && e < E) ? hi - lo : 0;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < kMaxBlocks; ++j) tab.cnt[j] = (j == 0 && lane == 0) ? p.M : 0;
   }
-  seg_scan(tab, nblk);
+  if constexpr (kSingle) {
+    tab.total_strips = strips_of(p.M);  // one segment: rows [0, M)
+  } else {
+    seg_scan(tab, nblk);
+  }
   if constexpr (MODE == kStripGrouped) {
     // rows keep the caller's offsets (the same as the prefix of the counts for
     // well-formed offsets; the caller's base is honoured)
@@ -396,15 +413,26 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
 
   const int total = tab.total_strips;
   int s0, s1;
-  {
+  if constexpr (kSingle) {
+    const StripRange range = even_range(total, grid, worker);
+    s0 = range.s0;
+    s1 = range.s1;
+  } else {
     const StripRange range = assign_strips(tab, nblk, E, total, grid, worker,
                                            MODE == kStripChain ? p.max_strips : INT_MAX);
     s0 = range.s0;
     s1 = range.s1;
   }
+  auto info = [&](int s) -> StripInfo {
+    if constexpr (kSingle) {
+      return StripInfo{0, s * kRows, p.M, s * kRows};
+    } else {
+      return strip_info(tab, nblk, E, s);
+    }
+  };
   StripInfo cur{};
   if (s0 < s1) {
-    cur = strip_info(tab, nblk, E, s0);
+    cur = info(s0);
     if constexpr (MODE == kStripGrouped) load_b(cur.e);  // in flight below
   }
 
@@ -538,6 +566,31 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
     }
   };
 
+  // ---- epilogue of one output row group: acc[r] is row 4g + r, column 16 wave + li ----
+  const int col = 16 * wave + li;
+  auto epilogue_row = [&](int r, const v4f& a, const StripInfo& st) {
+    const int rl = 4 * g + r;
+    if constexpr (MODE == kStripChain) {
+      const int32_t route = s_slot[st.rank0 + rl];  // st.rank0: slot of the strip's row 0
+      if (route >= 0 && col < N) {
+        p.C[static_cast<std::size_t>(st.row0 + rl) * N + col] = a[r];
+        // Both routes of a token add into the zeroed output: fl(0 + a) + b is
+        // the same in either order, so the combine is deterministic.
+        unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col,
+                        __fmul_rn(s_w[st.rank0 + rl], a[r]));
+      }
+    } else {
+      const int row = st.row0 + rl;
+      if (row < st.row_end && col < N) p.C[static_cast<std::size_t>(row) * N + col] = a[r];
+    }
+  };
+  // Deferred epilogues (all modes but the router, whose gate merge needs the
+  // whole strip at once).
+  constexpr bool kDeferred = MODE != kStripRouterGate;
+  v4f acc_prev = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+  StripInfo prev{};
+  bool pending = false;
+
   int cur_e = -1;
   int src = -1;
   if (s0 < s1) {
@@ -571,13 +624,16 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
     __syncthreads();
     // ---- prefetch the next strip's A rows (and B of its segment) ----
     if (s + 1 < s1) {
-      cur = strip_info(tab, nblk, E, s + 1);
+      cur = info(s + 1);
       src = a_source(s + 1, cur);
       load_a(src);
       if (cur.e != si.e) load_b(cur.e);
     }
 
     // ---- MFMA: acc = rows x columns [16 wave, 16 wave + 16) ----
+    // The previous strip's epilogue (kept in acc_prev) is issued between these
+    // MFMAs, one row per four k chunks, so its stores leave in the shadow of
+    // the matrix pipe instead of after it.
     v4f acc = v4f{0.0F, 0.0F, 0.0F, 0.0F};
     const float* aw = As + li * kLd + 4 * g;
     const float* bw = Bs + (16 * wave + li) * kLd + 4 * g;
@@ -591,29 +647,20 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
       }
-    }
-
-    // ---- epilogue: acc[r] is row 4g + r, column 16 wave + li ----
-    const int col = 16 * wave + li;
-    if constexpr (MODE == kStripChain) {
-      const int slot0 = (s - s0) * kRows;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rl = 4 * g + r;
-        const int32_t route = s_slot[slot0 + rl];
-        if (route < 0 || col >= N) continue;
-        const float w = s_w[slot0 + rl];
-        p.C[static_cast<std::size_t>(si.row0 + rl) * N + col] = acc[r];
-        // Both routes of a token add into the zeroed output: fl(0 + a) + b is
-        // the same in either order, so the combine is deterministic.
-        unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col, __fmul_rn(w, acc[r]));
+      if constexpr (kDeferred) {
+        if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
       }
+    }
+    if constexpr (kDeferred) {
+      // (rows 0..3 of the previous strip went out at c = 3, 7, 11, 15: the
+      // calls sit outside the c < chunks test, so short K emits them too)
+      acc_prev = acc;
+      prev = si;
+      prev.rank0 = (s - s0) * kRows;  // slot of the strip's first row (chain)
+      pending = true;
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = si.row0 + 4 * g + r;
-        if (row < si.row_end && col < N) p.C[static_cast<std::size_t>(row) * N + col] = acc[r];
-      }
+      for (int r = 0; r < 4; ++r) epilogue_row(r, acc, si);
     }
     if constexpr (MODE == kStripRouterGate) {
       // Top-2 of each row over its N logits: per wave over its 16 columns
@@ -658,6 +705,12 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
           for (int i = tid; i < n; i += kThreads) base[i] = 0.0F;
         }
       }
+    }
+  }
+  if constexpr (kDeferred) {
+    if (pending) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) epilogue_row(r, acc_prev, prev);
     }
   }
 }
