@@ -41,8 +41,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--stage-reps", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
-    ap.add_argument("--only", default="", help="comma list of extras to run: c3,c4,c4u,c5")
+    ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route")
     ap.add_argument("--profile", default="", choices=["", "headline", "c4"],
                     help="profiler driver: a fixed number of launches of one case, no timing, "
                          "no JSON line (for rocprofv3 --pmc / --kernel-trace runs)")
@@ -193,6 +192,55 @@ def time_loop(torch, fn, reps, warmup=3):
     return start.elapsed_time(stop) / 1e3 / reps
 
 
+def percentile(values, q):
+    """Linear interpolation between closest ranks (reference runner.cpp:42-50)."""
+    v = sorted(values)
+    if len(v) == 1:
+        return v[0]
+    pos = q * (len(v) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(v) - 1)
+    return v[lo] + (v[hi] - v[lo]) * (pos - lo)
+
+
+def sample_stats(seconds):
+    mean = statistics.fmean(seconds)
+    cv = statistics.pstdev(seconds) / mean if mean > 0 else 0.0
+    return {"samples": len(seconds), "p50_us": round(percentile(seconds, 0.5) * 1e6, 2),
+            "p95_us": round(percentile(seconds, 0.95) * 1e6, 2), "cv": round(cv, 4)}
+
+
+def batch_means(torch, fn, samples, repeats):
+    """Reference runner semantics (runner.cpp:283-411): each sample is one event
+    span over `repeats` back-to-back calls divided by `repeats`."""
+    out = []
+    for _ in range(samples):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(repeats):
+            fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b) / 1e3 / repeats)
+    return out
+
+
+def cold_spans(torch, ch, device, samples, scrub_mib=512):
+    """Single chains, each after a scrub of scrub_mib MiB written through the
+    caches (rr_launch_cache_scrub): the chain's working set (~60 MB) otherwise
+    stays in the 256 MB Infinity Cache between calls."""
+    scrub = torch.empty(scrub_mib << 18, dtype=torch.int32, device=device)
+    out = []
+    for _ in range(samples):
+        assert ch.rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), ch.stream) == 0
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(); ch.chain(); b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b) / 1e3)
+    del scrub
+    return out
+
+
 def stage_report(torch, ch, reps, model):
     out = {}
     for name in ch.stage_args:
@@ -240,6 +288,8 @@ def headline(torch, device, args):
         a.record(); ch.chain(); b.record()
         b.synchronize()
         spans.append(a.elapsed_time(b) / 1e3)
+    warm = sample_stats(batch_means(torch, ch.chain, samples=20, repeats=10))
+    cold = sample_stats(cold_spans(torch, ch, device, samples=20))
     active = int((ch.counts.cpu().numpy() > 0).sum())
     launches = launch_report(torch, ch, args.stage_reps,
                              fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
@@ -247,6 +297,7 @@ def headline(torch, device, args):
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, ch, args.stage_reps, model)
     return cfg, ch, inputs, {"elapsed_s": elapsed, "wall_s": wall, "p50_s": statistics.median(spans),
+                             "warm": warm, "cold": cold,
                              "launches": launches, "stages": stages, "active_experts": active}
 
 
@@ -300,6 +351,59 @@ def c5(torch, device, steps=20):
             "launches": launches, "stages": stages}
 
 
+def small_chain(torch, device, cfg, reps=200):
+    """C1 / C2 chain on the GPU (parity configs; timed for context)."""
+    from raggedroute_amd import workloads
+    inputs = workloads.chain_inputs(cfg, 0)
+    dev_inputs = {k: torch.from_numpy(v).to(device) for k, v in inputs.items()}
+    ch = Chain(cfg, dev_inputs, device)
+    sec = time_loop(torch, ch.chain, reps, warmup=10)
+    stats = sample_stats(batch_means(torch, ch.chain, samples=20, repeats=10))
+    del ch, dev_inputs
+    return {"T": cfg.tokens, "E": cfg.experts, "K": cfg.hidden, "N": cfg.output,
+            "entry": "chain_from_tokens" if cfg.from_tokens else "chain_from_logits",
+            "chain_us": round(sec * 1e6, 2), "tokens_per_s": round(cfg.tokens / sec, 1), "warm": stats}
+
+
+def route_chain(torch, device, reps=200):
+    """chain_from_route_ids at the reference's post-route release shapes
+    (representative / large for top_k 2, 4, 8 and max_route_pairs), uniform ids."""
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    stream = torch.cuda.current_stream(device).cuda_stream
+    out = {}
+    for name, cfg in workloads.route_chain_configs().items():
+        if name.startswith("small"):
+            continue
+        inp = workloads.route_chain_inputs(cfg, 0)
+        t, e, k, n, top = cfg.tokens, cfg.experts, cfg.hidden, cfg.output, cfg.top_k
+        r = t * top
+        d = {key: torch.from_numpy(np.ascontiguousarray(v)).to(device) for key, v in inp.items()}
+        i32 = dict(dtype=torch.int32, device=device)
+        bufs = {"counts": torch.empty(e, **i32), "offsets": torch.empty(e + 1, **i32),
+                "route_pos": torch.empty(r, **i32), "sorted_route": torch.empty(r, **i32),
+                "y_permuted": torch.empty(r, n, device=device), "y": torch.empty(t, n, device=device)}
+        args = rr.RouteChainArgs(
+            x=d["x"].data_ptr(), expert_ids=d["ids"].data_ptr(), route_weights=d["weights"].data_ptr(),
+            expert_weights=d["expert_weights"].data_ptr(), counts=bufs["counts"].data_ptr(),
+            offsets=bufs["offsets"].data_ptr(), x_permuted=None, route_pos=bufs["route_pos"].data_ptr(),
+            sorted_route=bufs["sorted_route"].data_ptr(), y_permuted=bufs["y_permuted"].data_ptr(),
+            y=bufs["y"].data_ptr(), tokens=t, experts=e, top_k=top, hidden=k, output=n)
+        ws = torch.empty(rr.get_route_chain_workspace_size(args) // 4, **i32)
+        ctx = rr.RuntimeContext(stream=stream, workspace=ws.data_ptr(), workspace_bytes=ws.numel() * 4,
+                                architecture=int(rr.DeviceArchitecture.kGfx950))
+
+        def call():
+            status = rr.chain_from_route_ids(args, ctx)
+            assert status.ok(), status.message
+        sec = time_loop(torch, call, reps, warmup=10)
+        out[name] = {"T": t, "E": e, "K": k, "N": n, "top_k": top, "us": round(sec * 1e6, 2),
+                     "tokens_per_s": round(t / sec, 1),
+                     "warm": sample_stats(batch_means(torch, call, samples=20, repeats=10))}
+        del d, bufs, ws
+    return out
+
+
 def c3(torch, device):
     import raggedroute_amd as rr
     from raggedroute_amd import workloads
@@ -321,17 +425,30 @@ def c3(torch, device):
     return out
 
 
-def cpu_baseline(inputs_host, budget_s):
+def cpu_chain_seconds(inputs_host, from_tokens, runs=5):
     """Reference CPU oracle chain (oracle/, single thread, -O2
-    -ffp-contract=off) on the full headline workload, median over repeats."""
+    -ffp-contract=off), median of `runs` full runs."""
     import oracle
-    runs = []
-    t_start = time.perf_counter()
-    while len(runs) < 25 and (len(runs) < 3 or time.perf_counter() - t_start < budget_s):
+    out = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        oracle.chain(inputs_host["x"], inputs_host["expert_weights"], router_weights=inputs_host["router_weights"])
-        runs.append(time.perf_counter() - t0)
-    return statistics.median(runs), len(runs)
+        if from_tokens:
+            oracle.chain(inputs_host["x"], inputs_host["expert_weights"],
+                         router_weights=inputs_host["router_weights"])
+        else:
+            oracle.chain(inputs_host["x"], inputs_host["expert_weights"], logits=inputs_host["logits"])
+        out.append(time.perf_counter() - t0)
+    return statistics.median(out)
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def profile(torch, device, case):
@@ -392,7 +509,12 @@ def main() -> int:
 
     extras = {}
     if not args.quick:
-        only = set(filter(None, args.only.split(","))) or {"c3", "c4", "c4u", "c5"}
+        only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c4u", "c5", "route"}
+        from raggedroute_amd import workloads
+        if "c1" in only:
+            extras["C1"] = small_chain(torch, device, workloads.C1)
+        if "c2" in only:
+            extras["C2"] = small_chain(torch, device, workloads.C2)
         if "c4" in only:
             extras["C4"] = c4(torch, device)
         if "c4u" in only:
@@ -401,15 +523,25 @@ def main() -> int:
             extras["C5"] = c5(torch, device)
         if "c3" in only:
             extras["C3"] = c3(torch, device)
+        if "route" in only:
+            extras["route_chain"] = route_chain(torch, device)
 
     cpu = None
     if not args.quick:
+        from raggedroute_amd import workloads
         host = {k: v.cpu().numpy() for k, v in inputs.items()}
-        sec, runs = cpu_baseline(host, args.cpu_seconds)
+        sec = cpu_chain_seconds(host, True)
+        others = {}
+        for c in (workloads.C1, workloads.C2):
+            sec_c = cpu_chain_seconds(workloads.chain_inputs(c, 0), c.from_tokens)
+            others[c.name] = {"tokens_per_s": round(c.tokens / sec_c, 1), "chain_ms": round(sec_c * 1e3, 3),
+                              "entry": "chain_from_tokens" if c.from_tokens else "chain_from_logits"}
         cpu = {"value": round(cfg.tokens / sec, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"full headline chain_from_tokens (T={cfg.tokens}, E={cfg.experts}, K={cfg.hidden}, "
-                         f"N={cfg.output}) on the oracle/ C restatement of the reference CPU chain, "
-                         f"median of {runs} runs", "host_cpus": os.cpu_count()}
+                         f"N={cfg.output}) on the oracle/ C restatement of the reference CPU chain "
+                         f"(single thread, -O2 -ffp-contract=off), median of 5 runs",
+               "chain_ms": round(sec * 1e3, 3), "configs": others, "cpu_model": cpu_model(),
+               "host_cpus": os.cpu_count(), "threads_used": 1}
 
     line = {
         "metric": "chain_from_tokens tokens/s @T4096/E64 FP32; grouped GEMM TFLOP/s; GB/s",
@@ -420,6 +552,8 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(head["elapsed_s"] / args.steps * 1e3, 4),
         "p50_chain_us": round(head["p50_s"] * 1e6, 2),
+        "chain_warm": head["warm"],
+        "chain_cold": head["cold"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -79,4 +79,61 @@ inline Status chain_from_logits(const ChainArgs& args, const RuntimeContext& con
   return detail::from_c(rr_chain_from_logits(&a, &c));
 }
 
+// Post-route chain (reference chain_from_route_ids suite,
+// benchmarks/adapters/postroute_chain_adapter.cpp:250-356).
+struct RouteChainArgs {
+  const float* x = nullptr;               // [tokens, hidden]
+  const std::int32_t* expert_ids = nullptr;  // [tokens, top_k]
+  const float* route_weights = nullptr;   // [tokens, top_k]
+  const float* expert_weights = nullptr;  // [experts, hidden, output]
+  std::int32_t* counts = nullptr;         // [experts]
+  std::int32_t* offsets = nullptr;        // [experts + 1]
+  float* x_permuted = nullptr;            // [tokens * top_k, hidden]; optional (auto / optimized)
+  std::int32_t* route_pos = nullptr;      // [tokens * top_k]
+  std::int32_t* sorted_route = nullptr;   // [tokens * top_k], optional
+  float* y_permuted = nullptr;            // [tokens * top_k, output]
+  float* y = nullptr;                     // [tokens, output]
+  int tokens = 0;
+  int experts = 0;
+  int top_k = 2;
+  int hidden = 0;
+  int output = 0;
+  KernelSelection kernel;
+};
+
+namespace detail {
+inline rr_route_chain_args to_c(const RouteChainArgs& a) noexcept {
+  rr_route_chain_args c{};
+  c.x = a.x;
+  c.expert_ids = a.expert_ids;
+  c.route_weights = a.route_weights;
+  c.expert_weights = a.expert_weights;
+  c.counts = a.counts;
+  c.offsets = a.offsets;
+  c.x_permuted = a.x_permuted;
+  c.route_pos = a.route_pos;
+  c.sorted_route = a.sorted_route;
+  c.y_permuted = a.y_permuted;
+  c.y = a.y;
+  c.tokens = a.tokens;
+  c.experts = a.experts;
+  c.top_k = a.top_k;
+  c.hidden = a.hidden;
+  c.output = a.output;
+  c.kernel = to_c(a.kernel);
+  return c;
+}
+}  // namespace detail
+
+inline std::size_t get_route_chain_workspace_size(const RouteChainArgs& args) noexcept {
+  const auto c = detail::to_c(args);
+  return rr_route_chain_workspace_size(&c);
+}
+
+inline Status chain_from_route_ids(const RouteChainArgs& args, const RuntimeContext& context) noexcept {
+  const auto a = detail::to_c(args);
+  const auto c = detail::to_c(context);
+  return detail::from_c(rr_chain_from_route_ids(&a, &c));
+}
+
 }  // namespace raggedroute

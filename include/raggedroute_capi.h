@@ -263,6 +263,34 @@ typedef struct rr_chain_args {
   rr_kernel_selection kernel; /* applied to every stage */
 } rr_chain_args;
 
+/*
+ * Post-route chain arguments: prepared route ids and weights -> histogram +
+ * exclusive scan -> token permute -> grouped GEMM -> unpermute. The reference
+ * runs this chain only as its chain_from_route_ids research suite (reference
+ * benchmarks/adapters/postroute_chain_adapter.cpp:142-230 setup, :250-356
+ * stages, :357-385 validation; top_k in {2, 4, 8}, top_k <= E).
+ */
+typedef struct rr_route_chain_args {
+  const float* x;              /* [tokens, hidden] */
+  const int32_t* expert_ids;   /* [tokens, top_k], each in [0, experts) */
+  const float* route_weights;  /* [tokens, top_k] */
+  const float* expert_weights; /* [experts, hidden, output] */
+  int32_t* counts;             /* [experts] */
+  int32_t* offsets;            /* [experts + 1] */
+  float* x_permuted;           /* [tokens * top_k, hidden]; optional on the auto / optimized
+                                  path (NULL: rows are gathered, not materialised) */
+  int32_t* route_pos;          /* [tokens * top_k] */
+  int32_t* sorted_route;       /* [tokens * top_k], optional */
+  float* y_permuted;           /* [tokens * top_k, output] */
+  float* y;                    /* [tokens, output] */
+  int32_t tokens;
+  int32_t experts;
+  int32_t top_k; /* 1..8, <= experts */
+  int32_t hidden;
+  int32_t output;
+  rr_kernel_selection kernel; /* applied to every stage */
+} rr_route_chain_args;
+
 /* reference include/raggedroute/operators.h:114-122 (get_*_workspace_size) */
 size_t rr_dense_gemm_workspace_size(const rr_dense_gemm_args* args);
 size_t rr_topk_gate_workspace_size(const rr_topk_gate_args* args);
@@ -276,6 +304,9 @@ size_t rr_unpermute_workspace_size(const rr_unpermute_args* args);
 /* no reference counterpart (chain entries are new): (experts + 2 * tokens)
  * int32 words = permute cursors + sorted_route scratch for the fused path */
 size_t rr_chain_workspace_size(const rr_chain_args* args);
+/* no reference counterpart (new entry): (experts + tokens * top_k) int32
+ * words = permute cursors + sorted_route scratch */
+size_t rr_route_chain_workspace_size(const rr_route_chain_args* args);
 
 /* reference include/raggedroute/operators.h:127 / src/dense_gemm/operator.cpp:18-58 */
 rr_status rr_dense_gemm(const rr_dense_gemm_args* args, const rr_runtime_context* context);
@@ -299,6 +330,15 @@ rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* 
  * sequence of reference benchmarks/adapters/chain_adapter.cpp:263-467. */
 rr_status rr_chain_from_tokens(const rr_chain_args* args, const rr_runtime_context* context);
 rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_context* context);
+/* No reference counterpart as a function: the stage sequence of the
+ * reference's chain_from_route_ids suite (reference
+ * benchmarks/adapters/postroute_chain_adapter.cpp:250-356). Auto / optimized:
+ * route preparation + gathered expert GEMM in one launch where the strip
+ * kernel covers the shape, then the rank-order unpermute; naive: the stage
+ * operators one by one (x_permuted required). Output y within the reference's
+ * tolerance (atol 1e-4, rtol 4e-5 * K * top_k, :381). */
+rr_status rr_chain_from_route_ids(const rr_route_chain_args* args,
+                                  const rr_runtime_context* context);
 /* No reference counterpart: timing hook. Runs one launch of the fused
  * (auto / optimized) chain alone so that a profiler or benchmark can time it
  * with events on the context's stream. Launches are numbered in execution

@@ -63,6 +63,7 @@ def _load() -> ctypes.CDLL:
         "rro_unpermute_f64": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "rro_unpermute_f32": (c_int, [vp, vp, vp, c_int, c_int, c_int, vp]),
         "rro_chain_output_f32": (None, [vp, vp, vp, vp, c_int, c_int, c_int, vp]),
+        "rro_route_chain_output_f32": (None, [vp, vp, vp, vp, c_int, c_int, c_int, c_int, vp]),
         "rro_chain": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int, c_int, c_int, vp, vp, vp, vp, vp, vp]),
         "rro_compare_floating": (c_int64, [vp, vp, c_int64, c_double, c_double, POINTER(c_double), POINTER(c_double)]),
         "rro_compare_gemm": (c_int64, [vp, vp, vp, vp, c_int, c_int, c_int, POINTER(c_double), POINTER(c_double)]),
@@ -224,6 +225,31 @@ def chain_output_f32(x, expert_weights, ids, route_weights):
     y = np.empty((t, o), np.float32)
     _lib.rro_chain_output_f32(_p(x), _p(we), _p(ids), _p(rw), t, h, o, _p(y))
     return y
+
+
+def route_chain_output_f32(x, expert_weights, ids, route_weights):
+    """Combined output of any top_k routes per token, FP32 in the reference's
+    loop order (reference benchmarks/adapters/postroute_chain_adapter.cpp:655-676)."""
+    x = _c(x, np.float32); we = _c(expert_weights, np.float32)
+    ids = _c(ids, np.int32); rw = _c(route_weights, np.float32)
+    t, h = x.shape; o = we.shape[2]
+    top_k = ids.shape[1]
+    y = np.empty((t, o), np.float32)
+    _lib.rro_route_chain_output_f32(_p(x), _p(we), _p(ids), _p(rw), t, top_k, h, o, _p(y))
+    return y
+
+
+def route_chain(x, expert_weights, ids, route_weights):
+    """Post-route chain oracle (reference benchmarks/adapters/postroute_chain_adapter.cpp:
+    678-700 and validate :357-385): counts and offsets of the route ids (adapter_utils.h:
+    324-342), the stable route map (the build's order, D1) and the combined output."""
+    ids = _c(ids, np.int32)
+    e = expert_weights.shape[0]
+    counts = histogram(ids, e)
+    offsets = exclusive_scan(counts)
+    pos = stable_route_pos(ids, offsets)
+    return {"counts": counts, "offsets": offsets, "route_pos": pos, "sorted_route": inverse_route(pos),
+            "y": route_chain_output_f32(x, expert_weights, ids, route_weights)}
 
 
 def chain(x, expert_weights, *, router_weights=None, logits=None):

@@ -336,14 +336,20 @@ int rro_unpermute_f32(const float* y_permuted, const int32_t* route_pos, const f
 
 /* reference benchmarks/adapters/chain_adapter.cpp:858-879: direct per-token
  * expert projection (sequential k) and weighted top-2 combine in FP32. */
-void rro_chain_output_f32(const float* x, const float* expert_weights, const int32_t* ids,
-                          const float* route_weights, int tokens, int hidden, int output,
-                          float* y) {
+/* Combined expert output of top_k routes per token, FP32 in the reference's
+ * loop order: per token and column, combined = 0; for each rank in order,
+ * projection = sequential FP32 dot of x[t] with column c of W[id]; combined +=
+ * weight * projection (reference benchmarks/adapters/chain_adapter.cpp:858-879
+ * for top-2, benchmarks/adapters/postroute_chain_adapter.cpp:655-676 for any
+ * top_k). */
+void rro_route_chain_output_f32(const float* x, const float* expert_weights, const int32_t* ids,
+                                const float* route_weights, int tokens, int top_k, int hidden,
+                                int output, float* y) {
   for (int t = 0; t < tokens; ++t) {
     for (int c = 0; c < output; ++c) {
       float combined = 0.0F;
-      for (int rank = 0; rank < 2; ++rank) {
-        const int64_t route = (int64_t)t * 2 + rank;
+      for (int rank = 0; rank < top_k; ++rank) {
+        const int64_t route = (int64_t)t * top_k + rank;
         const int64_t e = ids[route];
         float projection = 0.0F;
         for (int p = 0; p < hidden; ++p) {
@@ -354,6 +360,12 @@ void rro_chain_output_f32(const float* x, const float* expert_weights, const int
       y[(int64_t)t * output + c] = combined;
     }
   }
+}
+
+void rro_chain_output_f32(const float* x, const float* expert_weights, const int32_t* ids,
+                          const float* route_weights, int tokens, int hidden, int output,
+                          float* y) {
+  rro_route_chain_output_f32(x, expert_weights, ids, route_weights, tokens, 2, hidden, output, y);
 }
 
 /* The reference chain oracle in order (reference chain_adapter.cpp:188-239):

@@ -58,6 +58,9 @@ int rro_unpermute_f64(const double* y_permuted, const int32_t* route_pos,
                       const double* route_weights, int tokens, int top_k, int output, double* y);
 int rro_unpermute_f32(const float* y_permuted, const int32_t* route_pos, const float* route_weights,
                       int tokens, int top_k, int output, float* y);
+void rro_route_chain_output_f32(const float* x, const float* expert_weights, const int32_t* ids,
+                                const float* route_weights, int tokens, int top_k, int hidden,
+                                int output, float* y);
 void rro_chain_output_f32(const float* x, const float* expert_weights, const int32_t* ids,
                           const float* route_weights, int tokens, int hidden, int output,
                           float* y);

@@ -35,6 +35,7 @@ from ._capi import (  # noqa: F401  (re-exported vocabulary)
     MutableTensorView,
     OperatorKind,
     OperatorSignature,
+    RouteChainArgs,
     RuntimeContext,
     ScalarType,
     Status,
@@ -107,6 +108,14 @@ def chain_from_tokens(args: ChainArgs, context: RuntimeContext | None = None) ->
 
 def chain_from_logits(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
     return lib.rr_chain_from_logits(byref(args), byref(_ctx(context)))
+
+
+def chain_from_route_ids(args: RouteChainArgs, context: RuntimeContext | None = None) -> Status:
+    return lib.rr_chain_from_route_ids(byref(args), byref(_ctx(context)))
+
+
+def get_route_chain_workspace_size(args: RouteChainArgs) -> int:
+    return lib.rr_route_chain_workspace_size(byref(args))
 
 
 def chain_fused_launch(args: ChainArgs, context: RuntimeContext | None, from_tokens: bool,

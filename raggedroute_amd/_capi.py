@@ -223,6 +223,32 @@ class UnpermuteArgs(ctypes.Structure):
     ]
 
 
+class RouteChainArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p),
+        ("expert_ids", c_void_p),
+        ("route_weights", c_void_p),
+        ("expert_weights", c_void_p),
+        ("counts", c_void_p),
+        ("offsets", c_void_p),
+        ("x_permuted", c_void_p),
+        ("route_pos", c_void_p),
+        ("sorted_route", c_void_p),
+        ("y_permuted", c_void_p),
+        ("y", c_void_p),
+        ("tokens", c_int32),
+        ("experts", c_int32),
+        ("top_k", c_int32),
+        ("hidden", c_int32),
+        ("output", c_int32),
+        ("kernel", KernelSelection),
+    ]
+
+    def __init__(self, **kw):
+        kw.setdefault("top_k", 2)
+        super().__init__(**kw)
+
+
 class ChainArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p),
@@ -302,6 +328,8 @@ PROTOTYPES += [
     ("rr_chain_from_tokens", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_from_logits", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_fused_launch", Status, [POINTER(ChainArgs), POINTER(RuntimeContext), c_int32, c_int32]),
+    ("rr_chain_from_route_ids", Status, [POINTER(RouteChainArgs), POINTER(RuntimeContext)]),
+    ("rr_route_chain_workspace_size", c_size_t, [POINTER(RouteChainArgs)]),
     ("rr_chain_fused_launch_name", c_char_p, [POINTER(ChainArgs), c_int32, c_int32]),
     ("rr_classify_compute_capability", c_int32, [c_int32, c_int32]),
     ("rr_classify_gcn_arch_name", c_int32, [c_char_p]),

@@ -55,12 +55,14 @@ struct GemmParams {
   int dense_rows;
   int K;
   int N;
-  // kChainGrouped: segment row r holds token sorted_route[r] / 2 of X; the
-  // gathered rows go to x_permuted and y_out[token] += route_weights[route] * Y[r].
+  // kChainGrouped: segment row r holds token sorted_route[r] / top_k of X; the
+  // gathered rows go to x_permuted (when given) and, when y_out is given
+  // (top-2), y_out[token] += route_weights[route] * Y[r].
   const int32_t* sorted_route;
   const float* route_weights;
   float* x_permuted;
   float* y_out;
+  int top_k;
 };
 
 template <int BM_, int BN_, int WM_, int WN_, int BK_>
@@ -282,8 +284,8 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         float w = 0.0F;
         if (row < row_end) {
           const int32_t route = prm.sorted_route[row];
-          token = route >> 1;  // top-2: route = 2 * token + rank
-          w = prm.route_weights[route];
+          token = route / prm.top_k;  // route = top_k * token + rank
+          if (prm.y_out != nullptr) w = prm.route_weights[route];
         }
         s_src[r] = token;
         s_w[r] = w;
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
       __syncthreads();
       src_rows = s_src;
     }
-    const bool write_xp = MODE == kChainGrouped && ct == 0;
+    const bool write_xp = MODE == kChainGrouped && ct == 0 && prm.x_permuted != nullptr;
 
     v4f acc[S::kTM][S::kTN];
 #pragma unroll
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         float* comb = nullptr;
         float w = 0.0F;
         if constexpr (MODE == kChainGrouped) {
-          comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
+          if (prm.y_out != nullptr) comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
           w = s_w[rl];
         }
 #pragma unroll
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
               // Both routes of a token add into the zeroed output: fl(0 + a) + b
               // is the same in either order, so the combine is deterministic
               // and equals the rank-order unpermute.
-              unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
+              if (comb != nullptr) unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
             }
           }
         }
@@ -566,14 +568,16 @@ hipError_t router_gate_mfma(const float* x, const float* router_weights, float* 
 hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const int32_t* offsets,
                               const int32_t* sorted_route, const float* route_weights,
                               float* x_permuted, float* y_permuted, float* y, int tokens,
-                              int experts, int hidden, int output, hipStream_t stream) {
+                              int top_k, int experts, int hidden, int output, hipStream_t stream) {
   if (tokens <= 0 || output <= 0) return hipSuccess;
+  if (y != nullptr && top_k != 2) return hipErrorInvalidValue;  // combine is top-2 only
   GemmParams p = base_params(x, expert_weights, offsets, y_permuted, experts, 0, hidden, output);
   p.sorted_route = sorted_route;
   p.route_weights = route_weights;
   p.x_permuted = x_permuted;
   p.y_out = y;
-  const long routes = 2L * tokens;
+  p.top_k = top_k;
+  const long routes = static_cast<long>(tokens) * top_k;
   return gemm_dispatch<kChainGrouped>(p, routes, routes, stream);
 }
 

@@ -25,13 +25,14 @@ hipError_t grouped_gemm_mfma(const float* x, const float* w, const int32_t* offs
 hipError_t router_gate_mfma(const float* x, const float* router_weights, float* logits,
                             int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
                             int tokens, int experts, int hidden, hipStream_t stream);
-// Grouped GEMM over x rows gathered through sorted_route (top-2 routes): writes
-// x_permuted and y_permuted, and adds w[route] * y_permuted[row] into the
-// zeroed y[token] (the unpermute).
+// Grouped GEMM over x rows gathered through sorted_route (route = top_k *
+// token + rank): writes x_permuted (optional) and y_permuted and, when y is
+// given (top_k = 2 only), adds w[route] * y_permuted[row] into the zeroed
+// y[token] (the unpermute).
 hipError_t chain_grouped_mfma(const float* x, const float* expert_weights, const int32_t* offsets,
                               const int32_t* sorted_route, const float* route_weights,
                               float* x_permuted, float* y_permuted, float* y, int tokens,
-                              int experts, int hidden, int output, hipStream_t stream);
+                              int top_k, int experts, int hidden, int output, hipStream_t stream);
 
 // ---- narrow-output strip GEMMs (strip.hip): N <= 128, K <= 256 ----
 // Shape / alignment test shared by the strip entries (K and N multiples of 4,
@@ -41,8 +42,8 @@ bool strip_shape_ok(int k, int n, const void* a, const void* w);
 bool strip_segments_ok(int segments);
 // The fused route preparation + expert GEMM also needs T <= 8192, E <= 256 and
 // the route-id stage to fit in LDS.
-bool strip_chain_ok(int tokens, int experts, int k, int n, const void* x, const void* w,
-                    const void* ids, const void* x_permuted);
+bool strip_chain_ok(int tokens, int top_k, int experts, int k, int n, const void* x,
+                    const void* w, const void* ids, const void* x_permuted);
 hipError_t strip_dense(const float* a, const float* b, float* c, int m, int n, int k,
                        hipStream_t stream);
 // rows_bound: upper bound on the total segment rows (sizes the grid only).
@@ -51,14 +52,15 @@ hipError_t strip_grouped(const float* x, const float* w, const int32_t* offsets,
 hipError_t strip_router_gate(const float* x, const float* router_weights, float* logits,
                              int32_t* ids, float* gate_weights, float* y_zero, int y_cols,
                              int tokens, int experts, int hidden, hipStream_t stream);
-// ids (top-2 routes of every token, all in [0, experts)) -> counts, offsets,
-// cursors, stable route_pos, sorted_route (optional), x_permuted, y_permuted,
-// and y += w * y_permuted (y zeroed beforehand) in one launch.
+// ids (top_k routes of every token, all in [0, experts)) -> counts, offsets,
+// cursors, stable route_pos, sorted_route (optional), x_permuted (optional),
+// y_permuted and, when y is given (top_k = 2 only), y += w * y_permuted with
+// y zeroed beforehand, in one launch.
 hipError_t strip_chain(const float* x, const float* expert_weights, const int32_t* ids,
                        const float* route_weights, int32_t* counts, int32_t* offsets,
                        int32_t* cursors, int32_t* route_pos, int32_t* sorted_route,
-                       float* x_permuted, float* y_permuted, float* y, int tokens, int experts,
-                       int hidden, int output, hipStream_t stream);
+                       float* x_permuted, float* y_permuted, float* y, int tokens, int top_k,
+                       int experts, int hidden, int output, hipStream_t stream);
 
 // ---- routing kernels (routing.hip) ----
 // y_zero (optional): [tokens, y_cols] rows zeroed by the same launch (chain fusion).

@@ -62,6 +62,14 @@ size_t rr_chain_workspace_size(const rr_chain_args* args) {
   return (static_cast<size_t>(args->experts) + 2 * static_cast<size_t>(args->tokens)) *
          sizeof(int32_t);
 }
+// Route chain workspace: E cursor words, then T * top_k words that hold
+// sorted_route when the caller passes none.
+size_t rr_route_chain_workspace_size(const rr_route_chain_args* args) {
+  if (args == nullptr || args->experts <= 0 || args->tokens < 0 || args->top_k <= 0) return 0;
+  return (static_cast<size_t>(args->experts) +
+          static_cast<size_t>(args->tokens) * static_cast<size_t>(args->top_k)) *
+         sizeof(int32_t);
+}
 
 // reference src/dense_gemm/operator.cpp:18-58
 rr_status rr_dense_gemm(const rr_dense_gemm_args* args, const rr_runtime_context* context) {

@@ -29,10 +29,11 @@
 //                    compacts the routes of its own strips in stable (route
 //                    index) order with wave ballots, writes their
 //                    route_pos / sorted_route entries, gathers the token rows
-//                    of x (written to x_permuted), stores y_permuted and adds
-//                    w * y_permuted into the zeroed y (top-2: fl(0 + a) + b is
-//                    the same in either order, so the combine is deterministic
-//                    and equals the rank-order unpermute).
+//                    of x (written to x_permuted when given), stores
+//                    y_permuted and, for top-2 chains, adds w * y_permuted
+//                    into the zeroed y (fl(0 + a) + b is the same in either
+//                    order, so that combine is deterministic and equals the
+//                    rank-order unpermute). Any top_k: route = top_k * token + rank.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -77,6 +78,8 @@ struct StripParams {
   float* y_zero;
   int y_cols;
   // chain
+  int top_k;    // routes per token (route = top_k * token + rank)
+  int combine;  // 1: y[token] += w * y_permuted row (top-2, y zeroed before)
   const int32_t* ids;
   const float* route_weights;
   int32_t* counts;
@@ -84,8 +87,8 @@ struct StripParams {
   int32_t* cursors;
   int32_t* route_pos;
   int32_t* sorted_route;  // optional
-  float* x_permuted;
-  float* y;
+  float* x_permuted;  // optional
+  float* y;           // combine only
 };
 
 // Always-issued 16-byte load (ptr is clamped in bounds by the caller) with the
@@ -350,7 +353,9 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
     for (int u = 0; u < kIdChunks; ++u) {
       const int r = (c_begin + u) * 256 + 4 * lane;
       const bool full = c_begin + u < c_end && r + 3 < R;
-      const int4 v = *reinterpret_cast<const int4*>(p.ids + (full ? r : 0));
+      // (no vector read at all when R < 4: it would pass the end of ids)
+      const int4 v = R >= 4 ? *reinterpret_cast<const int4*>(p.ids + (full ? r : 0))
+                            : make_int4(-1, -1, -1, -1);
       idv[u] = full ? v : make_int4(-1, -1, -1, -1);
       if (c_begin + u < c_end && r < R && r + 3 >= R) {  // the ragged tail (R % 4 != 0)
         idv[u].x = p.ids[r];
@@ -535,7 +540,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       if (route >= 0) {
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
-        w_pending = p.route_weights[route];
+        if (p.combine) w_pending = p.route_weights[route];
       }
     }
   }
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
     if constexpr (MODE == kStripChain) {
       (void)si;
       const int32_t route = s_slot[(s - s0) * kRows + a_row];
-      return route >= 0 ? (route >> 1) : -1;  // top-2: route = 2 * token + rank
+      return route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
     } else {
       (void)s;
       const int row = si.row0 + a_row;
@@ -574,10 +579,12 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       const int32_t route = s_slot[st.rank0 + rl];  // st.rank0: slot of the strip's row 0
       if (route >= 0 && col < N) {
         p.C[static_cast<std::size_t>(st.row0 + rl) * N + col] = a[r];
-        // Both routes of a token add into the zeroed output: fl(0 + a) + b is
-        // the same in either order, so the combine is deterministic.
-        unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col,
-                        __fmul_rn(s_w[st.rank0 + rl], a[r]));
+        if (p.combine) {
+          // Both routes of a token add into the zeroed output: fl(0 + a) + b
+          // is the same in either order, so the combine is deterministic.
+          unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col,
+                          __fmul_rn(s_w[st.rank0 + rl], a[r]));
+        }
       }
     } else {
       const int row = st.row0 + rl;
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       if (k < chunks * 16) *reinterpret_cast<v4f*>(As + a_row * kLd + k) = a_regs[u];
     }
     if constexpr (MODE == kStripChain) {
-      if (src >= 0) {  // gathered rows -> x_permuted
+      if (src >= 0 && p.x_permuted != nullptr) {  // gathered rows -> x_permuted
         float* out = p.x_permuted + static_cast<std::size_t>(si.row0 + a_row) * K;
 #pragma unroll
         for (int u = 0; u < kALoads; ++u) {
@@ -813,11 +820,12 @@ bool strip_shape_ok(int k, int n, const void* a, const void* w) {
 
 bool strip_segments_ok(int segments) { return segments >= 1 && segments <= kMaxBlocks * 64; }
 
-bool strip_chain_ok(int tokens, int experts, int k, int n, const void* x, const void* w,
-                    const void* ids, const void* x_permuted) {
+bool strip_chain_ok(int tokens, int top_k, int experts, int k, int n, const void* x,
+                    const void* w, const void* ids, const void* x_permuted) {
   if (!strip_shape_ok(k, n, x, w) || !aligned16(ids) || !aligned16(x_permuted)) return false;
-  if (!strip_segments_ok(experts) || tokens <= 0 || tokens > 8192) return false;
-  const long routes = 2L * tokens;
+  if (!strip_segments_ok(experts) || tokens <= 0 || top_k < 1) return false;
+  const long routes = static_cast<long>(tokens) * top_k;
+  if (routes > kMaxRoutes) return false;
   const long bound = (routes + kRows - 1) / kRows + experts;
   const int grid = grid_for(bound);
   // strips per workgroup: up to ceil(bound / grid) in even contiguous ranges
@@ -857,14 +865,17 @@ hipError_t strip_router_gate(const float* x, const float* router_weights, float*
 hipError_t strip_chain(const float* x, const float* expert_weights, const int32_t* ids,
                        const float* route_weights, int32_t* counts, int32_t* offsets,
                        int32_t* cursors, int32_t* route_pos, int32_t* sorted_route,
-                       float* x_permuted, float* y_permuted, float* y, int tokens, int experts,
-                       int hidden, int output, hipStream_t stream) {
+                       float* x_permuted, float* y_permuted, float* y, int tokens, int top_k,
+                       int experts, int hidden, int output, hipStream_t stream) {
   if (tokens <= 0) return hipSuccess;
-  const int routes = 2 * tokens;
+  if (y != nullptr && top_k != 2) return hipErrorInvalidValue;  // combine is top-2 only
+  const int routes = tokens * top_k;
   StripParams p = base(x, expert_weights, y_permuted, routes, hidden, output, experts);
   const long bound = (static_cast<long>(routes) + kRows - 1) / kRows + experts;
   const int grid = grid_for(bound);
   p.max_strips = static_cast<int>((bound + grid - 1) / grid) + 1;
+  p.top_k = top_k;
+  p.combine = y != nullptr ? 1 : 0;
   p.ids = ids;
   p.route_weights = route_weights;
   p.counts = counts;

@@ -205,3 +205,103 @@ def chain_inputs_device(cfg: ChainConfig, seed: int, device) -> dict:
         x[:, k - 1] = 1.0
         wr[k - 1, :] = torch.from_numpy(expert_bias(e, cfg.logit_bias_s, seed)).to(device)
     return {"x": x, "expert_weights": we, "router_weights": wr}
+
+
+# ---- post-route chain (chain_from_route_ids) ----
+
+ROUTE_DISTRIBUTIONS = ("uniform", "zipf", "single_hot", "round_robin", "duplicate_route")
+
+
+def topk_route_ids(tokens: int, top_k: int, experts: int, distribution: str, seed: int,
+                   s: float = 1.4) -> np.ndarray:
+    """[tokens, top_k] expert ids with the distributions of reference
+    include/raggedroute/benchmark/adapter_utils.h:206-248: uniform / zipf
+    (p ~ (e + 1)^-s) draws redrawn until distinct inside the token;
+    single_hot = rank; round_robin = (token + rank) mod E; duplicate_route =
+    all zeros. Draws come from this module's counter stream, not mt19937_64."""
+    if tokens < 1 or top_k < 1 or experts < top_k:
+        raise ValueError("route shape requires tokens>=1 and experts>=top_k>=1")
+    rank = np.arange(top_k, dtype=np.int64)[None, :]
+    token = np.arange(tokens, dtype=np.int64)[:, None]
+    if distribution == "duplicate_route":
+        return np.zeros((tokens, top_k), np.int32)
+    if distribution == "single_hot":
+        return np.broadcast_to(rank, (tokens, top_k)).astype(np.int32)
+    if distribution == "round_robin":
+        return ((token + rank) % experts).astype(np.int32)
+    if distribution not in ("uniform", "zipf"):
+        raise ValueError(f"unsupported distribution: {distribution}")
+
+    def draw(u):
+        return (np.minimum((u * experts).astype(np.int64), experts - 1).astype(np.int32)
+                if distribution == "uniform" else zipf_draw(u, experts, s))
+
+    ids = np.empty((tokens, top_k), np.int32)
+    start = 0
+    for r in range(top_k):
+        col = draw(unit_doubles(tokens, seed, S_IDS, start))
+        start += tokens
+        bad = np.nonzero((ids[:, :r] == col[:, None]).any(axis=1))[0]
+        while bad.size:
+            col[bad] = draw(unit_doubles(bad.size, seed, S_IDS, start))
+            start += bad.size
+            bad = bad[(ids[bad, :r] == col[bad, None]).any(axis=1)]
+        ids[:, r] = col
+    return ids
+
+
+def topk_route_weights(tokens: int, top_k: int, seed: int) -> np.ndarray:
+    """U(0.01, 1) weights normalised per token in float32, rank order
+    (reference benchmarks/adapters/postroute_chain_adapter.cpp:684-694)."""
+    w = uniform(tokens * top_k, seed, S_WEIGHTS, 0.01, 1.0).reshape(tokens, top_k)
+    out = np.empty_like(w)
+    total = np.zeros(tokens, np.float32)
+    for r in range(top_k):
+        total = (total + w[:, r]).astype(np.float32)
+    for r in range(top_k):
+        out[:, r] = (w[:, r] / total).astype(np.float32)
+    return out
+
+
+@dataclass(frozen=True)
+class RouteChainConfig:
+    name: str
+    tokens: int
+    experts: int
+    hidden: int
+    output: int
+    top_k: int
+    distribution: str = "uniform"
+    zipf_s: float = 1.4
+
+    @property
+    def routes(self) -> int:
+        return self.tokens * self.top_k
+
+
+def route_chain_configs() -> dict:
+    """The reference's post-route release cases
+    (configs/project/benchmark/six_ops_v4_postroute_release.json): small
+    T64/E16/K64/N64, representative T512/E64/K128/N128, large
+    T2048/E64/K128/N128 for top_k 2, 4, 8, and max_route_pairs
+    T8192/E64/K64/N64 top_k 8."""
+    out = {}
+    for name, t, e, k, n in (("small", 64, 16, 64, 64), ("representative", 512, 64, 128, 128),
+                             ("large", 2048, 64, 128, 128)):
+        for top_k in (2, 4, 8):
+            cfg = RouteChainConfig(f"{name}.topk{top_k}", t, e, k, n, top_k)
+            out[cfg.name] = cfg
+    out["max_route_pairs.topk8"] = RouteChainConfig("max_route_pairs.topk8", 8192, 64, 64, 64, 8)
+    return out
+
+
+def route_chain_inputs(cfg: RouteChainConfig, seed: int = 0) -> dict:
+    """Host inputs: X ~ U(-1, 1), expert W ~ U(-1, 1) (the reference's
+    make_random_floats range), ids and weights as above."""
+    t, e, k, n = cfg.tokens, cfg.experts, cfg.hidden, cfg.output
+    return {
+        "x": uniform(t * k, seed, S_X).reshape(t, k),
+        "expert_weights": uniform(e * k * n, seed, S_EXPERTS).reshape(e, k, n),
+        "ids": topk_route_ids(t, cfg.top_k, e, cfg.distribution, seed, cfg.zipf_s),
+        "weights": topk_route_weights(t, cfg.top_k, seed),
+    }

@@ -252,6 +252,34 @@ def test_workspace_contracts():
     assert rr.get_chain_workspace_size(chain) == (8 + 2 * 4) * 4
     assert rr.chain_from_logits(chain, ctx).code == S.kInsufficientWorkspace
     assert rr.chain_from_tokens(rr.ChainArgs(tokens=0, experts=8), ctx).ok()
+    # N = 0: y, y_permuted and the expert weights have no elements (null is
+    # accepted); the call reaches the workspace check
+    chain = rr.ChainArgs(tokens=4, experts=8, hidden=4, output=0, logits=addr, expert_ids=addr,
+                         route_weights=addr, counts=addr, offsets=addr, route_pos=addr, x=addr,
+                         x_permuted=addr, router_weights=addr)
+    assert rr.chain_from_tokens(chain, ctx).code == S.kInsufficientWorkspace
+
+    # post-route chain: stage limits 1 <= top_k <= E <= 1024, top_k <= 64
+    for bad in (dict(top_k=0), dict(top_k=9, experts=8), dict(experts=0), dict(experts=1025),
+                dict(top_k=65, experts=128), dict(hidden=-1), dict(output=-1), dict(tokens=-1),
+                dict(tokens=2**28, top_k=8)):
+        route = rr.RouteChainArgs(**({"tokens": 4, "experts": 8, "top_k": 2, "hidden": 4, "output": 4} | bad))
+        assert rr.chain_from_route_ids(route, ctx).code == S.kInvalidArgument, bad
+    route = rr.RouteChainArgs(tokens=4, experts=8, top_k=8, hidden=4, output=4)
+    assert rr.chain_from_route_ids(route, ctx).code == S.kInvalidArgument  # null pointers
+    route = rr.RouteChainArgs(tokens=4, experts=8, top_k=8, hidden=4, output=4, x=addr, expert_ids=addr,
+                              route_weights=addr, expert_weights=addr, counts=addr, offsets=addr,
+                              route_pos=addr, y_permuted=addr, y=addr)
+    assert rr.get_route_chain_workspace_size(route) == (8 + 4 * 8) * 4
+    assert rr.chain_from_route_ids(route, ctx).code == S.kInsufficientWorkspace
+    assert rr.chain_from_route_ids(rr.RouteChainArgs(tokens=0, experts=8, top_k=4), ctx).ok()
+    route = rr.RouteChainArgs(tokens=4, experts=8, top_k=2, hidden=4, output=0, x=addr, expert_ids=addr,
+                              counts=addr, offsets=addr, route_pos=addr)
+    assert rr.chain_from_route_ids(route, ctx).code == S.kInsufficientWorkspace
+    route.hidden = 0
+    route.x = None
+    assert rr.chain_from_route_ids(route, ctx).code == S.kInsufficientWorkspace
+    assert rr.get_route_chain_workspace_size(rr.RouteChainArgs(experts=8, top_k=0)) == 0
 
 
 def test_naive_launchers_zero_size_contract():

@@ -387,3 +387,72 @@ def test_route_trace_fixture_metadata(kat):
         offsets = oracle.exclusive_scan(counts)
         pos = oracle.stable_route_pos(ids, offsets)
         assert sorted(pos.tolist()) == list(range(ids.size))
+
+
+# --------------------------------------------------------- post-route chain
+
+def test_route_chain_hand_kat():
+    """Hand-computed 2-token, top_k=3 case (E=3: identity, 2*identity, swap)."""
+    x = np.array([[1, 2], [3, 4]], np.float32)
+    we = np.stack([np.eye(2), 2 * np.eye(2), np.array([[0, 1], [1, 0]])]).astype(np.float32)
+    ids = np.array([[0, 1, 2], [2, 1, 0]], np.int32)
+    w = np.array([[0.5, 0.25, 0.25], [0.2, 0.3, 0.5]], np.float32)
+    out = oracle.route_chain(x, we, ids, w)
+    # token 0: .5*[1,2] + .25*[2,4] + .25*[2,1]; token 1: .2*[4,3] + .3*[6,8] + .5*[3,4]
+    np.testing.assert_allclose(out["y"], [[1.5, 2.25], [4.1, 5.0]], rtol=0, atol=1e-6)
+    assert out["counts"].tolist() == [2, 2, 2] and out["offsets"].tolist() == [0, 2, 4, 6]
+    # stable placement: routes 0 (t0 e0), 5 (t1 e0) -> 0, 1; 1, 4 -> 2, 3; 2, 3 -> 4, 5
+    assert out["route_pos"].tolist() == [0, 2, 4, 5, 3, 1]
+    assert out["sorted_route"].tolist() == [0, 5, 1, 4, 2, 3]
+
+
+@pytest.mark.parametrize("top_k,distribution", [(2, "uniform"), (4, "zipf"), (8, "uniform"),
+                                                (4, "duplicate_route"), (8, "round_robin")])
+def test_route_chain_closed_form(top_k, distribution):
+    from raggedroute_amd import workloads
+    cfg = workloads.RouteChainConfig("t", 17, 16, 64, 24, top_k, distribution)
+    inp = workloads.route_chain_inputs(cfg, seed=5)
+    out = oracle.route_chain(inp["x"], inp["expert_weights"], inp["ids"], inp["weights"])
+    ids = inp["ids"]
+    assert np.array_equal(out["counts"], np.bincount(ids.reshape(-1), minlength=16))
+    assert np.array_equal(out["offsets"], np.concatenate([[0], np.cumsum(out["counts"])]))
+    assert np.array_equal(out["route_pos"],
+                          np.argsort(np.argsort(ids.reshape(-1), kind="stable"), kind="stable"))
+    x64 = inp["x"].astype(np.float64); we64 = inp["expert_weights"].astype(np.float64)
+    w64 = inp["weights"].astype(np.float64)
+    expect = sum(w64[:, r:r + 1] * np.einsum("th,tho->to", x64, we64[ids[:, r]]) for r in range(top_k))
+    # reference tolerance of the post-route output (postroute_chain_adapter.cpp:381)
+    fails, _, _ = oracle.compare_floating(out["y"], expect, 1e-4, 4e-5 * cfg.hidden * top_k)
+    assert fails == 0
+    np.testing.assert_allclose(out["y"], expect, rtol=1e-5, atol=1e-5)
+
+
+def test_route_chain_top2_is_the_chain_output():
+    from raggedroute_amd import workloads
+    cfg = workloads.ChainConfig("tiny", 5, 4, 7, 5)  # reference tests/correctness_tests.cpp:788-802 shape
+    inp = workloads.chain_inputs(cfg, seed=1)
+    full = oracle.chain(inp["x"], inp["expert_weights"], router_weights=inp["router_weights"])
+    out = oracle.route_chain(inp["x"], inp["expert_weights"], full["ids"], full["weights"])
+    for key in ("counts", "offsets", "route_pos", "y"):
+        assert np.array_equal(out[key], full[key]), key
+
+
+def test_route_id_generator_contract():
+    """Distribution contract of reference adapter_utils.h:206-248."""
+    from raggedroute_amd import workloads
+    for dist in ("uniform", "zipf"):
+        ids = workloads.topk_route_ids(2000, 8, 16, dist, seed=3)
+        assert ids.min() >= 0 and ids.max() < 16
+        assert all(len(set(row)) == 8 for row in ids.tolist())
+    zipf = workloads.topk_route_ids(4000, 1, 16, "zipf", seed=4, s=1.4).reshape(-1)
+    counts = np.bincount(zipf, minlength=16)
+    assert counts[0] > counts[1] > counts[3] > counts[15]  # p ~ (e + 1)^-1.4
+    assert np.array_equal(workloads.topk_route_ids(3, 4, 8, "single_hot", 0), np.tile(np.arange(4), (3, 1)))
+    rr_ids = workloads.topk_route_ids(5, 2, 3, "round_robin", 0)
+    assert rr_ids.tolist() == [[0, 1], [1, 2], [2, 0], [0, 1], [1, 2]]
+    assert not workloads.topk_route_ids(4, 4, 4, "duplicate_route", 0).any()
+    with pytest.raises(ValueError):
+        workloads.topk_route_ids(4, 5, 4, "uniform", 0)
+    w = workloads.topk_route_weights(100, 8, seed=2)
+    assert w.dtype == np.float32 and (w > 0).all()
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-5)
