@@ -55,6 +55,18 @@ int main() {
   chain.experts = 8;
   chain.top_k = 3;
   expect(chain_from_tokens(chain, context).code == StatusCode::kInvalidArgument, "chain top_k");
+
+  RouteChainArgs route;
+  route.tokens = 4;
+  route.experts = 8;
+  route.top_k = 4;
+  route.hidden = 16;
+  route.output = 16;
+  expect(get_route_chain_workspace_size(route) == (8 + 4 * 4) * sizeof(std::int32_t),
+         "route chain workspace query");
+  route.top_k = 9;
+  expect(chain_from_route_ids(route, context).code == StatusCode::kInvalidArgument,
+         "route chain top_k > E");
   expect(ops::launch_dense_gemm_naive(nullptr, nullptr, nullptr, 0, 5, 3, nullptr) == hipSuccess,
          "empty naive dense GEMM is a no-op");
 
