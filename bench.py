@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--stage-reps", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
-    ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route")
+    ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route,trace")
+    ap.add_argument("--route-trace", default="", help="replay every frame of this .rrtrace file (extras.route_trace)")
     ap.add_argument("--profile", default="", choices=["", "headline", "c4"],
                     help="profiler driver: a fixed number of launches of one case, no timing, "
                          "no JSON line (for rocprofv3 --pmc / --kernel-trace runs)")
@@ -404,6 +405,66 @@ def route_chain(torch, device, reps=200):
     return out
 
 
+def trace_replay(torch, device, path=None, hidden=256, output=128, reps=100):
+    """Route-trace replay: every frame of a `.rrtrace` file (read by the
+    library's native reader) through chain_from_logits (top_k = 2: logits that
+    select the frame's ids) and chain_from_route_ids. Without a path: a
+    generated T4096 / E64 trace with uniform, Zipf(1.4), round-robin and
+    single-hot frames (every token on experts 0 and 1)."""
+    import tempfile
+    import raggedroute_amd as rr
+    from raggedroute_amd import route_trace, workloads
+    tmp = None
+    if path is None:
+        tmp = tempfile.TemporaryDirectory()
+        frames = {d.replace("zipf", "zipf1.4"): workloads.topk_route_ids(4096, 2, 64, d, seed=i)
+                  for i, d in enumerate(("uniform", "zipf", "round_robin", "single_hot"))}
+        doc = route_trace.document("generated_t4096_e64", "synthetic_fixture", 64, frames)
+        path = Path(tmp.name) / "generated.rrtrace"
+        path.write_text(route_trace.normalized_text(doc))
+    out = {}
+    stream = torch.cuda.current_stream(device).cuda_stream
+    for tr in route_trace.read_all(path):
+        t, e, top = tr.tokens, tr.experts, tr.top_k
+        rec = {"T": t, "E": e, "top_k": top, "K": hidden, "N": output,
+               "max_expert_routes": int(np.bincount(tr.ids.reshape(-1), minlength=e).max())}
+        if top == 2:
+            cfg = workloads.ChainConfig(tr.frame_id, t, e, hidden, output, from_tokens=False)
+            host = workloads.chain_inputs(cfg, 0)
+            host["logits"] = route_trace.logits_for_ids(tr.ids, e)
+            ch = Chain(cfg, {k: torch.from_numpy(v).to(device) for k, v in host.items()}, device)
+            sec = time_loop(torch, ch.chain, reps, warmup=10)
+            rec["chain_from_logits_us"] = round(sec * 1e6, 2)
+            del ch
+        rcfg = workloads.RouteChainConfig(tr.frame_id, t, e, hidden, output, top)
+        inp = workloads.route_chain_inputs(rcfg, 0)
+        d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(device) for k, v in inp.items()}
+        d["ids"] = torch.from_numpy(tr.ids).to(device)
+        i32 = dict(dtype=torch.int32, device=device)
+        r = t * top
+        bufs = [torch.empty(e, **i32), torch.empty(e + 1, **i32), torch.empty(r, **i32),
+                torch.empty(r, output, device=device), torch.empty(t, output, device=device)]
+        args = rr.RouteChainArgs(x=d["x"].data_ptr(), expert_ids=d["ids"].data_ptr(),
+                                 route_weights=d["weights"].data_ptr(),
+                                 expert_weights=d["expert_weights"].data_ptr(), counts=bufs[0].data_ptr(),
+                                 offsets=bufs[1].data_ptr(), route_pos=bufs[2].data_ptr(),
+                                 y_permuted=bufs[3].data_ptr(), y=bufs[4].data_ptr(), tokens=t, experts=e,
+                                 top_k=top, hidden=hidden, output=output)
+        ws = torch.empty(rr.get_route_chain_workspace_size(args) // 4, **i32)
+        ctx = rr.RuntimeContext(stream=stream, workspace=ws.data_ptr(), workspace_bytes=ws.numel() * 4,
+                                architecture=int(rr.DeviceArchitecture.kGfx950))
+
+        def call():
+            status = rr.chain_from_route_ids(args, ctx)
+            assert status.ok(), status.message
+        rec["chain_from_route_ids_us"] = round(time_loop(torch, call, reps, warmup=10) * 1e6, 2)
+        out[tr.frame_id] = rec
+        del d, bufs, ws
+    if tmp is not None:
+        tmp.cleanup()
+    return {"trace": str(path) if tmp is None else "generated", "frames": out}
+
+
 def c3(torch, device):
     import raggedroute_amd as rr
     from raggedroute_amd import workloads
@@ -509,7 +570,7 @@ def main() -> int:
 
     extras = {}
     if not args.quick:
-        only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c4u", "c5", "route"}
+        only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c4u", "c5", "route", "trace"}
         from raggedroute_amd import workloads
         if "c1" in only:
             extras["C1"] = small_chain(torch, device, workloads.C1)
@@ -525,6 +586,10 @@ def main() -> int:
             extras["C3"] = c3(torch, device)
         if "route" in only:
             extras["route_chain"] = route_chain(torch, device)
+        if "trace" in only:
+            extras["route_trace"] = trace_replay(torch, device, args.route_trace or None)
+    elif args.route_trace:
+        extras["route_trace"] = trace_replay(torch, device, args.route_trace)
 
     cpu = None
     if not args.quick:

@@ -291,6 +291,20 @@ typedef struct rr_route_chain_args {
   rr_kernel_selection kernel; /* applied to every stage */
 } rr_route_chain_args;
 
+/*
+ * Route trace (.rrtrace text format v1; reference
+ * include/raggedroute/benchmark/adapter_utils.h:250-256 RouteTraceFrame).
+ */
+typedef struct rr_route_trace_info {
+  int32_t tokens;
+  int32_t experts; /* 1..1024 (the reference caps traces at 64) */
+  int32_t top_k;
+  int32_t frame_count;
+  char trace_id[128];   /* truncated copies, NUL-terminated */
+  char source_kind[32]; /* production | captured | synthetic_fixture */
+  char frame_id[128];   /* of the frame read */
+} rr_route_trace_info;
+
 /* reference include/raggedroute/operators.h:114-122 (get_*_workspace_size) */
 size_t rr_dense_gemm_workspace_size(const rr_dense_gemm_args* args);
 size_t rr_topk_gate_workspace_size(const rr_topk_gate_args* args);
@@ -339,6 +353,14 @@ rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_conte
  * tolerance (atol 1e-4, rtol 4e-5 * K * top_k, :381). */
 rr_status rr_chain_from_route_ids(const rr_route_chain_args* args,
                                   const rr_runtime_context* context);
+/* reference include/raggedroute/benchmark/adapter_utils.h:269-322
+ * (load_route_trace_frame): validates the whole trace file at `path` and
+ * copies frame `frame`'s tokens * top_k expert ids (token-major, host memory)
+ * into expert_ids; expert_ids = NULL reads the header only. The reference's
+ * std::invalid_argument cases return RR_STATUS_INVALID_ARGUMENT with the same
+ * message (without the path). Host-only: no device call. */
+rr_status rr_route_trace_read(const char* path, int32_t frame, rr_route_trace_info* info,
+                              int32_t* expert_ids, size_t capacity);
 /* No reference counterpart: timing hook. Runs one launch of the fused
  * (auto / optimized) chain alone so that a profiler or benchmark can time it
  * with events on the context's stream. Launches are numbered in execution

@@ -36,6 +36,7 @@ from ._capi import (  # noqa: F401  (re-exported vocabulary)
     OperatorKind,
     OperatorSignature,
     RouteChainArgs,
+    RouteTraceInfo,
     RuntimeContext,
     ScalarType,
     Status,

@@ -223,6 +223,18 @@ class UnpermuteArgs(ctypes.Structure):
     ]
 
 
+class RouteTraceInfo(ctypes.Structure):
+    _fields_ = [
+        ("tokens", c_int32),
+        ("experts", c_int32),
+        ("top_k", c_int32),
+        ("frame_count", c_int32),
+        ("trace_id", ctypes.c_char * 128),
+        ("source_kind", ctypes.c_char * 32),
+        ("frame_id", ctypes.c_char * 128),
+    ]
+
+
 class RouteChainArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p),
@@ -329,6 +341,7 @@ PROTOTYPES += [
     ("rr_chain_from_logits", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_fused_launch", Status, [POINTER(ChainArgs), POINTER(RuntimeContext), c_int32, c_int32]),
     ("rr_chain_from_route_ids", Status, [POINTER(RouteChainArgs), POINTER(RuntimeContext)]),
+    ("rr_route_trace_read", Status, [ctypes.c_char_p, c_int32, POINTER(RouteTraceInfo), c_void_p, c_size_t]),
     ("rr_route_chain_workspace_size", c_size_t, [POINTER(RouteChainArgs)]),
     ("rr_chain_fused_launch_name", c_char_p, [POINTER(ChainArgs), c_int32, c_int32]),
     ("rr_classify_compute_capability", c_int32, [c_int32, c_int32]),

@@ -150,6 +150,16 @@ def main() -> None:
     path = Path(__file__).with_name("kat.json")
     path.write_text(json.dumps(kats, indent=1, sort_keys=True) + "\n")
     print(f"wrote {path}")
+    # The same fixture as a text trace, frames in the file's order (data, for the
+    # native reader's tests).
+    fx = kats["route_trace_fixture"]
+    lines = [fx["schema"], fx["trace_id"], fx["source_kind"],
+             f'{fx["tokens"]} {fx["experts"]} {fx["top_k"]} {len(fx["frames"])}']
+    for name in ("balanced", "skewed", "shifted"):
+        lines.append(name + " " + " ".join(str(v) for v in fx["frames"][name]))
+    trace = Path(__file__).with_name("synthetic_fixture.rrtrace")
+    trace.write_text("\n".join(lines) + "\n")
+    print(f"wrote {trace}")
 
 
 if __name__ == "__main__":
