@@ -242,6 +242,39 @@ def cold_spans(torch, ch, device, samples, scrub_mib=512):
     return out
 
 
+def graph_report(torch, device, ch, reps=200):
+    """The headline chain replayed from a captured graph (rr_chain_graph_*)
+    against direct calls: GPU time per chain (events over `reps` back-to-back
+    calls on one stream) and host time to submit one call (no synchronisation
+    inside the loop)."""
+    rr = ch.rr
+    stream = torch.cuda.Stream(device)
+    ctx = rr.RuntimeContext(stream=stream.cuda_stream, workspace=ch.ctx.workspace,
+                            workspace_bytes=ch.ctx.workspace_bytes, architecture=ch.ctx.architecture)
+    entry = rr.CHAIN_FROM_TOKENS if ch.cfg.from_tokens else rr.CHAIN_FROM_LOGITS
+    fn = rr.chain_from_tokens if ch.cfg.from_tokens else rr.chain_from_logits
+
+    def direct():
+        status = fn(ch.chain_args, ctx)
+        assert status.ok(), status.message
+
+    out = {}
+    with rr.ChainGraph(entry, ch.chain_args, ctx) as graph, torch.cuda.stream(stream):
+        def replay():
+            status = graph.launch(stream.cuda_stream)
+            assert status.ok(), status.message
+        out["kernel_nodes"] = graph.kernel_nodes
+        for name, call in (("direct", direct), ("graph", replay)):
+            out[f"{name}_us"] = round(time_loop(torch, call, reps, warmup=10) * 1e6, 2)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                call()
+            out[f"{name}_submit_us"] = round((time.perf_counter() - t0) / reps * 1e6, 2)
+            torch.cuda.synchronize()
+    return out
+
+
 def stage_report(torch, ch, reps, model):
     out = {}
     for name in ch.stage_args:
@@ -295,10 +328,11 @@ def headline(torch, device, args):
     launches = launch_report(torch, ch, args.stage_reps,
                              fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
     ch.chain()  # restore y (timing launch 2 alone keeps adding into it)
+    graph = graph_report(torch, device, ch)
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, ch, args.stage_reps, model)
     return cfg, ch, inputs, {"elapsed_s": elapsed, "wall_s": wall, "p50_s": statistics.median(spans),
-                             "warm": warm, "cold": cold,
+                             "warm": warm, "cold": cold, "graph": graph,
                              "launches": launches, "stages": stages, "active_experts": active}
 
 
@@ -619,6 +653,7 @@ def main() -> int:
         "p50_chain_us": round(head["p50_s"] * 1e6, 2),
         "chain_warm": head["warm"],
         "chain_cold": head["cold"],
+        "chain_graph": head["graph"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

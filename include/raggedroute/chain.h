@@ -136,4 +136,47 @@ inline Status chain_from_route_ids(const RouteChainArgs& args, const RuntimeCont
   return detail::from_c(rr_chain_from_route_ids(&a, &c));
 }
 
+// One chain call captured into an executable HIP graph (auto / optimized
+// family). Move-only owner of an rr_chain_graph.
+class ChainGraph {
+ public:
+  ChainGraph() = default;
+  ChainGraph(const ChainGraph&) = delete;
+  ChainGraph& operator=(const ChainGraph&) = delete;
+  ChainGraph(ChainGraph&& other) noexcept : graph_(other.graph_) { other.graph_ = nullptr; }
+  ChainGraph& operator=(ChainGraph&& other) noexcept {
+    if (this != &other) {
+      rr_chain_graph_destroy(graph_);
+      graph_ = other.graph_;
+      other.graph_ = nullptr;
+    }
+    return *this;
+  }
+  ~ChainGraph() { rr_chain_graph_destroy(graph_); }
+
+  Status capture_from_tokens(const ChainArgs& args, const RuntimeContext& context) noexcept {
+    return capture(RR_CHAIN_FROM_TOKENS, detail::to_c(args), context);
+  }
+  Status capture_from_logits(const ChainArgs& args, const RuntimeContext& context) noexcept {
+    return capture(RR_CHAIN_FROM_LOGITS, detail::to_c(args), context);
+  }
+  Status capture_from_route_ids(const RouteChainArgs& args, const RuntimeContext& context) noexcept {
+    return capture(RR_CHAIN_FROM_ROUTE_IDS, detail::to_c(args), context);
+  }
+  Status launch(hipStream_t stream) noexcept {
+    return detail::from_c(rr_chain_graph_launch(graph_, stream));
+  }
+  int kernel_nodes() const noexcept { return rr_chain_graph_kernel_nodes(graph_); }
+
+ private:
+  template <class CArgs>
+  Status capture(int entry, const CArgs& c_args, const RuntimeContext& context) noexcept {
+    rr_chain_graph_destroy(graph_);
+    graph_ = nullptr;
+    const auto c = detail::to_c(context);
+    return detail::from_c(rr_chain_graph_create(entry, &c_args, &c, &graph_));
+  }
+  rr_chain_graph* graph_ = nullptr;
+};
+
 }  // namespace raggedroute

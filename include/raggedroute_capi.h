@@ -361,6 +361,48 @@ rr_status rr_chain_from_route_ids(const rr_route_chain_args* args,
  * message (without the path). Host-only: no device call. */
 rr_status rr_route_trace_read(const char* path, int32_t frame, rr_route_trace_info* info,
                               int32_t* expert_ids, size_t capacity);
+/*
+ * Chain graphs. No reference counterpart as a library interface: the
+ * reference's CUDA-graph chain variants (benchmarks/adapters/chain_adapter.cpp:
+ * 730-826 fixed capture and exec update, :962-1000 LRU shape cache of 16;
+ * postroute_chain_adapter.cpp the same for the post-route chain) as objects.
+ * `args` points at an rr_chain_args (RR_CHAIN_FROM_TOKENS / _LOGITS) or an
+ * rr_route_chain_args (RR_CHAIN_FROM_ROUTE_IDS). Capture validates the call
+ * like the direct entry, records it on context->stream (must not be the
+ * default stream; nothing runs) and instantiates it; only the auto /
+ * optimized family is capturable. Kernel arguments are baked at capture: the
+ * buffers must outlive the graph, their contents are read at each replay.
+ * Not thread-safe.
+ */
+enum { RR_CHAIN_FROM_TOKENS = 0, RR_CHAIN_FROM_LOGITS = 1, RR_CHAIN_FROM_ROUTE_IDS = 2 };
+typedef struct rr_chain_graph rr_chain_graph;
+typedef struct rr_chain_graph_cache rr_chain_graph_cache;
+typedef struct rr_chain_graph_cache_stats {
+  int32_t capacity;
+  int32_t entries;
+  int64_t hits;
+  int64_t misses;
+} rr_chain_graph_cache_stats;
+
+rr_status rr_chain_graph_create(int32_t entry, const void* args, const rr_runtime_context* context,
+                                rr_chain_graph** graph);
+rr_status rr_chain_graph_launch(rr_chain_graph* graph, hipStream_t stream);
+/* Re-captures the graph's entry with new args (same entry) and updates the
+ * executable in place (hipGraphExecUpdate); a changed launch plan is
+ * instantiated anew. */
+rr_status rr_chain_graph_update(rr_chain_graph* graph, const void* args,
+                                const rr_runtime_context* context);
+int32_t rr_chain_graph_kernel_nodes(const rr_chain_graph* graph);
+void rr_chain_graph_destroy(rr_chain_graph* graph);
+/* Cache of executable graphs keyed by every pointer, size and kernel field of
+ * the call plus workspace and architecture; a miss captures the call, evicting
+ * the least recently used entry at capacity. */
+rr_status rr_chain_graph_cache_create(int32_t capacity, rr_chain_graph_cache** cache);
+rr_status rr_chain_graph_cache_launch(rr_chain_graph_cache* cache, int32_t entry, const void* args,
+                                      const rr_runtime_context* context);
+void rr_chain_graph_cache_get_stats(const rr_chain_graph_cache* cache, rr_chain_graph_cache_stats* stats);
+void rr_chain_graph_cache_destroy(rr_chain_graph_cache* cache);
+
 /* No reference counterpart: timing hook. Runs one launch of the fused
  * (auto / optimized) chain alone so that a profiler or benchmark can time it
  * with events on the context's stream. Launches are numbered in execution

@@ -20,7 +20,11 @@ from ._capi import (  # noqa: F401  (re-exported vocabulary)
     GFX950_NATIVE,
     MAX_EXPERTS,
     PROTOTYPES,
+    CHAIN_FROM_LOGITS,
+    CHAIN_FROM_ROUTE_IDS,
+    CHAIN_FROM_TOKENS,
     ChainArgs,
+    ChainGraphCacheStats,
     ConstTensorView,
     DenseGemmArgs,
     DeviceArchitecture,
@@ -134,6 +138,79 @@ def chain_fused_launch_names(args: ChainArgs, from_tokens: bool) -> list[str]:
         if name is None:
             return names
         names.append(name.decode())
+
+
+# ---- chain graphs (rr_chain_graph_*, rr_chain_graph_cache_*) ----
+
+class ChainGraph:
+    """One chain call captured into an executable HIP graph. `entry` is
+    CHAIN_FROM_TOKENS / CHAIN_FROM_LOGITS (ChainArgs) or CHAIN_FROM_ROUTE_IDS
+    (RouteChainArgs); raises RuntimeError with the library's message when the
+    call cannot be captured."""
+
+    def __init__(self, entry: int, args, context: RuntimeContext):
+        self._handle = ctypes.c_void_p()
+        self.entry = entry
+        st = lib.rr_chain_graph_create(entry, ctypes.addressof(args), byref(context), byref(self._handle))
+        if not st.ok():
+            raise RuntimeError(st.message)
+
+    def launch(self, stream) -> Status:
+        return lib.rr_chain_graph_launch(self._handle, stream)
+
+    def update(self, args, context: RuntimeContext) -> Status:
+        return lib.rr_chain_graph_update(self._handle, ctypes.addressof(args), byref(context))
+
+    @property
+    def kernel_nodes(self) -> int:
+        return lib.rr_chain_graph_kernel_nodes(self._handle)
+
+    def close(self) -> None:
+        if self._handle:
+            lib.rr_chain_graph_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+
+class ChainGraphCache:
+    """LRU cache of chain graphs keyed by the whole call (capacity 16 like the
+    reference's graph cache)."""
+
+    def __init__(self, capacity: int = 16):
+        self._handle = ctypes.c_void_p()
+        st = lib.rr_chain_graph_cache_create(capacity, byref(self._handle))
+        if not st.ok():
+            raise RuntimeError(st.message)
+
+    def launch(self, entry: int, args, context: RuntimeContext) -> Status:
+        return lib.rr_chain_graph_cache_launch(self._handle, entry, ctypes.addressof(args), byref(context))
+
+    def stats(self) -> ChainGraphCacheStats:
+        out = ChainGraphCacheStats()
+        lib.rr_chain_graph_cache_get_stats(self._handle, byref(out))
+        return out
+
+    def close(self) -> None:
+        if self._handle:
+            lib.rr_chain_graph_cache_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
 
 
 # ---- workspace queries (reference operators.h:114-122) ----

@@ -235,6 +235,13 @@ class RouteTraceInfo(ctypes.Structure):
     ]
 
 
+class ChainGraphCacheStats(ctypes.Structure):
+    _fields_ = [("capacity", c_int32), ("entries", c_int32), ("hits", c_int64), ("misses", c_int64)]
+
+
+CHAIN_FROM_TOKENS, CHAIN_FROM_LOGITS, CHAIN_FROM_ROUTE_IDS = 0, 1, 2
+
+
 class RouteChainArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p),
@@ -341,6 +348,15 @@ PROTOTYPES += [
     ("rr_chain_from_logits", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_fused_launch", Status, [POINTER(ChainArgs), POINTER(RuntimeContext), c_int32, c_int32]),
     ("rr_chain_from_route_ids", Status, [POINTER(RouteChainArgs), POINTER(RuntimeContext)]),
+    ("rr_chain_graph_create", Status, [c_int32, c_void_p, POINTER(RuntimeContext), POINTER(c_void_p)]),
+    ("rr_chain_graph_launch", Status, [c_void_p, c_void_p]),
+    ("rr_chain_graph_update", Status, [c_void_p, c_void_p, POINTER(RuntimeContext)]),
+    ("rr_chain_graph_kernel_nodes", c_int32, [c_void_p]),
+    ("rr_chain_graph_destroy", None, [c_void_p]),
+    ("rr_chain_graph_cache_create", Status, [c_int32, POINTER(c_void_p)]),
+    ("rr_chain_graph_cache_launch", Status, [c_void_p, c_int32, c_void_p, POINTER(RuntimeContext)]),
+    ("rr_chain_graph_cache_get_stats", None, [c_void_p, POINTER(ChainGraphCacheStats)]),
+    ("rr_chain_graph_cache_destroy", None, [c_void_p]),
     ("rr_route_trace_read", Status, [ctypes.c_char_p, c_int32, POINTER(RouteTraceInfo), c_void_p, c_size_t]),
     ("rr_route_chain_workspace_size", c_size_t, [POINTER(RouteChainArgs)]),
     ("rr_chain_fused_launch_name", c_char_p, [POINTER(ChainArgs), c_int32, c_int32]),
