@@ -91,11 +91,16 @@ struct StripParams {
   float* y;           // combine only
 };
 
-// Always-issued 16-byte load (ptr is clamped in bounds by the caller) with the
-// value replaced by zeros where !valid: a load under a condition becomes a
-// branch per load and a wait at every join, serialising the loads.
-__device__ __forceinline__ v4f load_or_zero(const float* ptr, bool valid) {
-  const v4f v = *reinterpret_cast<const v4f*>(ptr);
+// Always-issued 16-byte load from an address the caller clamps in bounds; the
+// caller replaces invalid values by zeros where it consumes them. A load under
+// a condition becomes a branch per load and a wait at every join; a select
+// right after the load waits for the data there. Prefetches keep the raw
+// value and select at the LDS store, after the work they overlap.
+__device__ __forceinline__ v4f load_raw(const float* ptr) {
+  return *reinterpret_cast<const v4f*>(ptr);
+}
+
+__device__ __forceinline__ v4f zero_unless(bool valid, const v4f& v) {
   return valid ? v : v4f{0.0F, 0.0F, 0.0F, 0.0F};
 }
 
@@ -258,13 +263,24 @@ __device__ __forceinline__ StripInfo strip_info(const SegTable& t, int nblk, int
   return si;
 }
 
-// One wave per 16 output columns: BN = 128 -> 8 waves, BN = 64 -> 4 waves.
-template <int BN>
-constexpr int strip_threads() { return BN / 16 * 64; }
+// Waves per workgroup: one per 16-column tile (BN / 16). The kernel also
+// runs with fewer waves, each owning BN / 16 / waves adjacent tiles (two
+// independent MFMA chains): at BN = 128, four waves of two tiles measured
+// 26.6 us for the headline chain's expert launch against 22.6 us for eight
+// waves of one tile; two waves per SIMD hide the LDS and memory latencies
+// that one wave exposes. The router needs one tile per wave (its gate merge
+// runs per wave).
+constexpr int kWaves128 = 8;
+constexpr int strip_waves(int bn, int mode) {
+  return mode == kStripRouterGate ? bn / 16 : (bn == 128 ? kWaves128 : 4);
+}
 
-template <int BN, int MODE, int CHUNKS>
-__global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(StripParams p) {
-  constexpr int kWaves = BN / 16;
+template <int BN, int WAVES, int MODE, int CHUNKS>
+__global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParams p) {
+  constexpr int kWaves = WAVES;
+  constexpr int kTiles = BN / 16 / WAVES;              // 16-column MFMA tiles per wave
+  static_assert(kTiles * 16 * WAVES == BN && (kTiles == 1 || kTiles == 2), "waves x tiles = BN / 16");
+  static_assert(MODE != kStripRouterGate || kTiles == 1, "the gate merge takes one tile per wave");
   constexpr int kThreads = kWaves * 64;
   constexpr int kNB = BN / 16;                         // 16-column blocks of B
   constexpr int kBLoads = kMaxChunks * kNB / kWaves;   // float4 B loads per lane (whole K)
@@ -316,7 +332,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       const int n = (blk % kNB) * 16 + 4 * bnq;
       const int kc = k < K ? k : K - 1;
       const int nc = n < N ? n : N - 4;
-      breg[u] = load_or_zero(W + static_cast<std::size_t>(kc) * N + nc, k < K && n < N);
+      breg[u] = load_raw(W + static_cast<std::size_t>(kc) * N + nc);
     }
   };
   auto store_b = [&]() {
@@ -327,10 +343,11 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
         const int k = (blk / kNB) * 16 + bks;
         const int n = (blk % kNB) * 16 + 4 * bnq;
         float* dst = Bs + n * kLd + k;
-        dst[0] = breg[u].x;
-        dst[kLd] = breg[u].y;
-        dst[2 * kLd] = breg[u].z;
-        dst[3 * kLd] = breg[u].w;
+        const v4f v = zero_unless(k < K && n < N, breg[u]);
+        dst[0] = v.x;
+        dst[kLd] = v.y;
+        dst[2 * kLd] = v.z;
+        dst[3 * kLd] = v.w;
       }
     }
   };
@@ -495,7 +512,11 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       for (int s = s0; s < s1 && i < kMaxSegs; ++i) {
         const Seg sg = seg_at(s);
         int32_t q = 0;
-        for (int w = 0; w < wave; ++w) q += s_misc[w * kMaxSegs + i];
+        // routes of this segment in the chunks of the waves before mine: one
+        // LDS read per lane and a wave sum (a loop of dependent reads costs
+        // one LDS round trip per earlier wave)
+        const int32_t earlier = s_misc[(lane < kWaves ? lane : 0) * kMaxSegs + i];
+        q = wave_sum(lane < wave ? earlier : 0);
 #pragma unroll
         for (int u = 0; u < kIdChunks; ++u) {
           if (c_begin + u < c_end && q < sg.hi) {
@@ -567,34 +588,54 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
 #pragma unroll
     for (int u = 0; u < kALoads; ++u) {
       const int k = 4 * (a_col + kRowThreads * u);
-      a_regs[u] = load_or_zero(row + (k < K ? k : K - 4), src >= 0 && k < K);
+      a_regs[u] = load_raw(row + (k < K ? k : K - 4));  // zeroed at the LDS store
     }
   };
 
-  // ---- epilogue of one output row group: acc[r] is row 4g + r, column 16 wave + li ----
-  const int col = 16 * wave + li;
-  auto epilogue_row = [&](int r, const v4f& a, const StripInfo& st) {
+  // ---- epilogue of one output row group: acc[t][r] is row 4g + r, column
+  // col0 + 16 t ----
+  const int col0 = 16 * kTiles * wave + li;
+  auto epilogue_row = [&](int r, const v4f (&a)[kTiles], const StripInfo& st) {
     const int rl = 4 * g + r;
     if constexpr (MODE == kStripChain) {
       const int32_t route = s_slot[st.rank0 + rl];  // st.rank0: slot of the strip's row 0
-      if (route >= 0 && col < N) {
-        p.C[static_cast<std::size_t>(st.row0 + rl) * N + col] = a[r];
+      if (route >= 0) {
+        float* crow = p.C + static_cast<std::size_t>(st.row0 + rl) * N;
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+          const int col = col0 + 16 * t;
+          if (col < N) crow[col] = a[t][r];
+        }
         if (p.combine) {
           // Both routes of a token add into the zeroed output: fl(0 + a) + b
           // is the same in either order, so the combine is deterministic.
-          unsafeAtomicAdd(p.y + static_cast<std::size_t>(route >> 1) * N + col,
-                          __fmul_rn(s_w[st.rank0 + rl], a[r]));
+          const float w = s_w[st.rank0 + rl];
+          float* yrow = p.y + static_cast<std::size_t>(route >> 1) * N;
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t) {
+            const int col = col0 + 16 * t;
+            if (col < N) unsafeAtomicAdd(yrow + col, __fmul_rn(w, a[t][r]));
+          }
         }
       }
     } else {
       const int row = st.row0 + rl;
-      if (row < st.row_end && col < N) p.C[static_cast<std::size_t>(row) * N + col] = a[r];
+      if (row < st.row_end) {
+        float* crow = p.C + static_cast<std::size_t>(row) * N;
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+          const int col = col0 + 16 * t;
+          if (col < N) crow[col] = a[t][r];
+        }
+      }
     }
   };
   // Deferred epilogues (all modes but the router, whose gate merge needs the
   // whole strip at once).
   constexpr bool kDeferred = MODE != kStripRouterGate;
-  v4f acc_prev = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+  v4f acc_prev[kTiles];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) acc_prev[t] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
   StripInfo prev{};
   bool pending = false;
 
@@ -615,7 +656,9 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
 #pragma unroll
     for (int u = 0; u < kALoads; ++u) {
       const int k = 4 * (a_col + kRowThreads * u);
-      if (k < chunks * 16) *reinterpret_cast<v4f*>(As + a_row * kLd + k) = a_regs[u];
+      if (k < chunks * 16) {
+        *reinterpret_cast<v4f*>(As + a_row * kLd + k) = zero_unless(src >= 0 && k < K, a_regs[u]);
+      }
     }
     if constexpr (MODE == kStripChain) {
       if (src >= 0 && p.x_permuted != nullptr) {  // gathered rows -> x_permuted
@@ -637,22 +680,31 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       if (cur.e != si.e) load_b(cur.e);
     }
 
-    // ---- MFMA: acc = rows x columns [16 wave, 16 wave + 16) ----
+    // ---- MFMA: acc[t] = rows x columns [col0 + 16 t - li, + 16) ----
     // The previous strip's epilogue (kept in acc_prev) is issued between these
     // MFMAs, one row per four k chunks, so its stores leave in the shadow of
-    // the matrix pipe instead of after it.
-    v4f acc = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+    // the matrix pipe instead of after it. With two tiles the chains
+    // alternate, each keeping its own k order.
+    v4f acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
     const float* aw = As + li * kLd + 4 * g;
-    const float* bw = Bs + (16 * wave + li) * kLd + 4 * g;
+    const float* bw = Bs + (16 * kTiles * wave + li) * kLd + 4 * g;
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
       if (c < chunks) {
         const v4f af = *reinterpret_cast<const v4f*>(aw + 16 * c);
-        const v4f bf = *reinterpret_cast<const v4f*>(bw + 16 * c);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
+        v4f bf[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) bf[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd + 16 * c);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[t].x, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf[t].y, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[t].z, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[t].w, acc[t], 0, 0, 0);
       }
       if constexpr (kDeferred) {
         if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
@@ -661,7 +713,8 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
     if constexpr (kDeferred) {
       // (rows 0..3 of the previous strip went out at c = 3, 7, 11, 15: the
       // calls sit outside the c < chunks test, so short K emits them too)
-      acc_prev = acc;
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) acc_prev[t] = acc[t];
       prev = si;
       prev.rank0 = (s - s0) * kRows;  // slot of the strip's first row (chain)
       pending = true;
@@ -677,7 +730,7 @@ __global__ __launch_bounds__(strip_threads<BN>(), 1) void rr_strip_gemm_kernel(S
       for (int r = 0; r < 4; ++r) {
         const int row = si.row0 + 4 * g + r;
         uint64_t k1 = 0, k2 = 0;
-        if (row < si.row_end && col < N) k1 = rr::dev::gate_key(acc[r], col);
+        if (row < si.row_end && col0 < N) k1 = rr::dev::gate_key(acc[0][r], col0);
         rr::dev::merge_top2_row16(k1, k2);
         if (li == 0) {
           s_keys[(wave * kRows + 4 * g + r) * 2] = k1;
@@ -758,7 +811,7 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   const int chunks = (K + 15) >> 4;
   const std::size_t stage = static_cast<std::size_t>(bn + kRows) * (chunks * 16 + 4);
   std::size_t bytes = stage * sizeof(float);
-  const int waves = bn / 16;
+  const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(waves) * kRows * 2 * sizeof(uint64_t);
   (void)segments;
   bytes += (kMaxBlocks * 64 + static_cast<std::size_t>(waves) * kMaxSegs) * sizeof(int32_t);
@@ -768,9 +821,10 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
 
 template <int BN, int MODE, int CHUNKS>
 hipError_t launch_strip_3(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
-  const hipError_t attr = allow_lds(rr_strip_gemm_kernel<BN, MODE, CHUNKS>);
+  constexpr int kWaves = strip_waves(BN, MODE);
+  const hipError_t attr = allow_lds(rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS>);
   if (attr != hipSuccess) return attr;
-  rr_strip_gemm_kernel<BN, MODE, CHUNKS><<<grid, strip_threads<BN>(), lds, stream>>>(p);
+  rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS><<<grid, kWaves * 64, lds, stream>>>(p);
   return hipGetLastError();
 }
 
