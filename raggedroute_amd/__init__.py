@@ -14,6 +14,16 @@ from __future__ import annotations
 
 import ctypes
 from ctypes import byref
+
+# One HIP runtime serves a process: the library binds whichever
+# libamdhip64.so.7 is loaded first. PyTorch-ROCm wheels bundle their own, and a
+# torch built for another ROCm release stops seeing the GPU when the system
+# runtime was loaded before it (the library works on either), so torch, when
+# installed, is loaded before the library.
+try:
+    import torch  # noqa: F401
+except ImportError:  # the library does not need it
+    pass
 from pathlib import Path
 
 from ._capi import (  # noqa: F401  (re-exported vocabulary)

@@ -14,6 +14,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch  # noqa: F401  (before the library: torch's bundled HIP runtime serves the process)
 
 REPO = Path(__file__).resolve().parent.parent
 if str(REPO) not in sys.path:
