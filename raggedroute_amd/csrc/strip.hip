@@ -303,7 +303,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   int32_t* s_cnt =
       reinterpret_cast<int32_t*>(s_keys + (MODE == kStripRouterGate ? kWaves * kRows * 2 : 0));
   int32_t* s_misc = s_cnt + kMaxBlocks * 64;    // [waves][kMaxSegs]
-  int32_t* s_slot = s_misc + kWaves * kMaxSegs; // chain: [max_strips * 16] route of each row
+  int32_t* s_seglist = s_misc + kWaves * kMaxSegs;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
+  int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 8 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
 
   const int tid = static_cast<int>(threadIdx.x);
@@ -463,82 +464,86 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   if constexpr (MODE == kStripChain) {
     const int slots = (s1 - s0) * kRows;
     for (int i = tid; i < slots; i += kThreads) s_slot[i] = -1;
-    // My segments, walked again in each pass (uniform values; runtime loops
-    // keep one copy of the unrolled chunk code): segment e covers my strips
-    // [s, last), i.e. its stable ranks [lo, hi), stored from slot base + rank.
-    struct Seg {
-      int e, lo, hi, base, off, last;
-    };
-    // Called in uniform control flow only (seg_find ballots over the wave).
-    auto seg_at = [&](int s) -> Seg {
-      Seg sg;
-      sg.e = seg_find(tab, nblk, E, s);
-      const int pre_e = seg_field(tab.pre, sg.e);
-      const int rows_e = seg_field(tab.cnt, sg.e);
-      const int end_e = pre_e + strips_of(rows_e);
-      sg.last = s1 < end_e ? s1 : end_e;
-      const int hi = (sg.last - pre_e) * kRows;
-      sg.lo = (s - pre_e) * kRows;
-      sg.hi = hi < rows_e ? hi : rows_e;
-      sg.base = (pre_e - s0) * kRows;
-      sg.off = seg_field(tab.off, sg.e);
-      return sg;
-    };
-    // pass 1: routes of each of my segments in this wave's chunks
+    // My segments: segment e covers my strips [s, last), i.e. its stable
+    // ranks [lo, hi), stored from slot base + rank. The walk (ballot lookups
+    // and readlanes, uniform control flow only) runs once per wave into the
+    // wave's own LDS rows; the passes read them back (LDS operations of one
+    // wave complete in order, so no barrier is needed).
+    int32_t* s_segs = s_seglist + wave * kMaxSegs * 8;  // [kMaxSegs][e, lo, hi, base, off]
+    int nseg = 0;
     {
-      int i = 0;
 #pragma unroll 1
-      for (int s = s0; s < s1 && i < kMaxSegs; ++i) {
-        const Seg sg = seg_at(s);
-        int32_t n = 0;
-#pragma unroll
-        for (int u = 0; u < kIdChunks; ++u) {
-          if (c_begin + u < c_end) {
-            n += __popcll(__ballot(idv[u].x == sg.e)) + __popcll(__ballot(idv[u].y == sg.e)) +
-                 __popcll(__ballot(idv[u].z == sg.e)) + __popcll(__ballot(idv[u].w == sg.e));
-          }
+      for (int s = s0; s < s1 && nseg < kMaxSegs; ++nseg) {
+        const int e = seg_find(tab, nblk, E, s);
+        const int pre_e = seg_field(tab.pre, e);
+        const int rows_e = seg_field(tab.cnt, e);
+        const int end_e = pre_e + strips_of(rows_e);
+        const int last = s1 < end_e ? s1 : end_e;
+        const int hi = (last - pre_e) * kRows;
+        const int off_e = seg_field(tab.off, e);
+        if (lane == 0) {
+          int32_t* d = s_segs + nseg * 8;
+          *reinterpret_cast<int4*>(d) =
+              make_int4(e, (s - pre_e) * kRows, hi < rows_e ? hi : rows_e, (pre_e - s0) * kRows);
+          d[4] = off_e;
         }
-        if (lane == 0) s_misc[wave * kMaxSegs + i] = n;
-        s = sg.last > s ? sg.last : s1;  // always advances
+        s = last > s ? last : s1;  // always advances
       }
     }
-    __syncthreads();
-    // pass 2: stable ranks (route order = wave, chunk, lane, component); keep
-    // the ones that fall in my strips
-    {
-      const uint64_t lt = lanemask_lt();
-      int i = 0;
+    struct Seg {
+      int e, lo, hi, base, off;
+    };
+    auto seg_read = [&](int i) -> Seg {
+      const int4 v = *reinterpret_cast<const int4*>(s_segs + i * 8);
+      return Seg{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w),
+                 __builtin_amdgcn_readfirstlane(s_segs[i * 8 + 4])};
+    };
+    auto matches = [](const int4& v, int e) -> int32_t {
+      return (v.x == e ? 1 : 0) + (v.y == e ? 1 : 0) + (v.z == e ? 1 : 0) + (v.w == e ? 1 : 0);
+    };
+    // pass 1: routes of each of my segments in this wave's chunks (per-lane
+    // match counts, one wave sum)
 #pragma unroll 1
-      for (int s = s0; s < s1 && i < kMaxSegs; ++i) {
-        const Seg sg = seg_at(s);
-        int32_t q = 0;
-        // routes of this segment in the chunks of the waves before mine: one
-        // LDS read per lane and a wave sum (a loop of dependent reads costs
-        // one LDS round trip per earlier wave)
-        const int32_t earlier = s_misc[(lane < kWaves ? lane : 0) * kMaxSegs + i];
-        q = wave_sum(lane < wave ? earlier : 0);
+    for (int i = 0; i < nseg; ++i) {
+      const Seg sg = seg_read(i);
+      int32_t n = 0;
 #pragma unroll
-        for (int u = 0; u < kIdChunks; ++u) {
-          if (c_begin + u < c_end && q < sg.hi) {
-            const uint64_t m0 = __ballot(idv[u].x == sg.e);
-            const uint64_t m1 = __ballot(idv[u].y == sg.e);
-            const uint64_t m2 = __ballot(idv[u].z == sg.e);
-            const uint64_t m3 = __ballot(idv[u].w == sg.e);
-            int rank = q + __popcll(m0 & lt) + __popcll(m1 & lt) + __popcll(m2 & lt) +
-                       __popcll(m3 & lt);
-            const int r = (c_begin + u) * 256 + 4 * lane;
-            const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+      for (int u = 0; u < kIdChunks; ++u) {
+        if (c_begin + u < c_end) n += matches(idv[u], sg.e);
+      }
+      n = wave_sum(n);
+      if (lane == 0) s_misc[wave * kMaxSegs + i] = n;
+    }
+    __syncthreads();
+    // pass 2: stable ranks (route order = wave, chunk, lane, component): the
+    // exclusive scan of the per-lane match counts over the wave gives each
+    // lane's first rank in a chunk; keep the ones that fall in my strips
+#pragma unroll 1
+    for (int i = 0; i < nseg; ++i) {
+      const Seg sg = seg_read(i);
+      // routes of this segment in the chunks of the waves before mine: one
+      // LDS read per lane and a wave sum (a loop of dependent reads costs
+      // one LDS round trip per earlier wave)
+      const int32_t earlier = s_misc[(lane < kWaves ? lane : 0) * kMaxSegs + i];
+      int32_t q = wave_sum(lane < wave ? earlier : 0);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              if (vals[k] == sg.e) {
-                if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = r + k;
-                ++rank;
-              }
+      for (int u = 0; u < kIdChunks; ++u) {
+        if (c_begin + u < c_end && q < sg.hi) {
+          const int32_t m = matches(idv[u], sg.e);
+          const int32_t incl = rr::dev::wave_inclusive_scan(m);
+          int rank = q + incl - m;
+          const int r = (c_begin + u) * 256 + 4 * lane;
+          const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (vals[k] == sg.e) {
+              if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = r + k;
+              ++rank;
             }
-            q += __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
           }
+          q += __builtin_amdgcn_readlane(incl, 63);
         }
-        s = sg.last > s ? sg.last : s1;  // always advances
       }
     }
     __syncthreads();
@@ -548,13 +553,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     if (s0 < s1) load_b(cur.e);
     // route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows
-    // (the walk runs in uniform control flow: seg_find's ballot needs every lane)
     int row = 0;
 #pragma unroll 1
-    for (int s = s0; s < s1;) {
-      const Seg sg = seg_at(s);
+    for (int i = 0; i < nseg; ++i) {
+      const Seg sg = seg_read(i);
       if (tid >= sg.base + sg.lo && tid < sg.base + sg.hi) row = sg.off + (tid - sg.base);
-      s = sg.last > s ? sg.last : s1;
     }
     if (tid < slots) {  // slots <= (kMaxSegs + 1) * 16 <= kThreads
       const int32_t route = s_slot[tid];
@@ -815,7 +818,10 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(waves) * kRows * 2 * sizeof(uint64_t);
   (void)segments;
   bytes += (kMaxBlocks * 64 + static_cast<std::size_t>(waves) * kMaxSegs) * sizeof(int32_t);
-  if (mode == kStripChain) bytes += 2 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);
+  if (mode == kStripChain) {
+    bytes += static_cast<std::size_t>(waves) * kMaxSegs * 8 * sizeof(int32_t);  // segment lists
+    bytes += 2 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);
+  }
   return bytes;
 }
 
