@@ -302,10 +302,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   uint64_t* s_keys = reinterpret_cast<uint64_t*>(As + kRows * kLd);  // router: [waves][16][2]
   int32_t* s_cnt =
       reinterpret_cast<int32_t*>(s_keys + (MODE == kStripRouterGate ? kWaves * kRows * 2 : 0));
-  int32_t* s_misc = s_cnt + kMaxBlocks * 64;    // [waves][kMaxSegs]
-  int32_t* s_seglist = s_misc + kWaves * kMaxSegs;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
+  int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 8 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
+  // chain: [waves][64 nblk] route-id histogram of each wave's chunks
+  int32_t* s_cntw = reinterpret_cast<int32_t*>(s_w + (MODE == kStripChain ? p.max_strips * kRows : 0));
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     const int nchunks = (R + 255) >> 8;
     c_begin = wave * nchunks / kWaves;
     c_end = (wave + 1) * nchunks / kWaves;
-    for (int e = tid; e < kMaxBlocks * 64; e += kThreads) s_cnt[e] = 0;
+    for (int i = tid; i < kWaves * 64 * nblk; i += kThreads) s_cntw[i] = 0;
 #pragma unroll
     for (int u = 0; u < kIdChunks; ++u) {
       const int r = (c_begin + u) * 256 + 4 * lane;
@@ -388,9 +389,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          if (static_cast<unsigned>(vals[k]) < static_cast<unsigned>(E)) atomicAdd(s_cnt + vals[k], 1);
+          if (static_cast<unsigned>(vals[k]) < static_cast<unsigned>(E)) {
+            atomicAdd(s_cntw + wave * 64 * nblk + vals[k], 1);  // this wave's own row
+          }
         }
       }
+    }
+    __syncthreads();
+    for (int e = tid; e < 64 * nblk; e += kThreads) {
+      int32_t total = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) total += s_cntw[w * 64 * nblk + e];
+      s_cnt[e] = total;
     }
     __syncthreads();
 #pragma unroll
@@ -502,30 +512,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     auto matches = [](const int4& v, int e) -> int32_t {
       return (v.x == e ? 1 : 0) + (v.y == e ? 1 : 0) + (v.z == e ? 1 : 0) + (v.w == e ? 1 : 0);
     };
-    // pass 1: routes of each of my segments in this wave's chunks (per-lane
-    // match counts, one wave sum)
+    // Stable ranks (route order = wave, chunk, lane, component): a segment's
+    // routes in the chunks of the waves before mine are the sum of those
+    // waves' histogram rows; inside a chunk, the exclusive scan of the
+    // per-lane match counts over the wave gives each lane's first rank. Keep
+    // the ranks that fall in my strips.
 #pragma unroll 1
     for (int i = 0; i < nseg; ++i) {
       const Seg sg = seg_read(i);
-      int32_t n = 0;
-#pragma unroll
-      for (int u = 0; u < kIdChunks; ++u) {
-        if (c_begin + u < c_end) n += matches(idv[u], sg.e);
-      }
-      n = wave_sum(n);
-      if (lane == 0) s_misc[wave * kMaxSegs + i] = n;
-    }
-    __syncthreads();
-    // pass 2: stable ranks (route order = wave, chunk, lane, component): the
-    // exclusive scan of the per-lane match counts over the wave gives each
-    // lane's first rank in a chunk; keep the ones that fall in my strips
-#pragma unroll 1
-    for (int i = 0; i < nseg; ++i) {
-      const Seg sg = seg_read(i);
-      // routes of this segment in the chunks of the waves before mine: one
-      // LDS read per lane and a wave sum (a loop of dependent reads costs
-      // one LDS round trip per earlier wave)
-      const int32_t earlier = s_misc[(lane < kWaves ? lane : 0) * kMaxSegs + i];
+      // (one LDS read per lane and a wave sum: a loop of dependent reads
+      // costs one LDS round trip per earlier wave)
+      const int32_t earlier = s_cntw[(lane < kWaves ? lane : 0) * 64 * nblk + sg.e];
       int32_t q = wave_sum(lane < wave ? earlier : 0);
 #pragma unroll
       for (int u = 0; u < kIdChunks; ++u) {
@@ -816,11 +813,11 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(waves) * kRows * 2 * sizeof(uint64_t);
-  (void)segments;
-  bytes += (kMaxBlocks * 64 + static_cast<std::size_t>(waves) * kMaxSegs) * sizeof(int32_t);
+  bytes += kMaxBlocks * 64 * sizeof(int32_t);
   if (mode == kStripChain) {
     bytes += static_cast<std::size_t>(waves) * kMaxSegs * 8 * sizeof(int32_t);  // segment lists
     bytes += 2 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);
+    bytes += static_cast<std::size_t>(waves) * 64 * ((segments + 63) / 64) * sizeof(int32_t);  // per-wave histograms
   }
   return bytes;
 }
