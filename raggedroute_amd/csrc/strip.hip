@@ -368,15 +368,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     c_begin = wave * nchunks / kWaves;
     c_end = (wave + 1) * nchunks / kWaves;
     for (int i = tid; i < kWaves * 64 * nblk; i += kThreads) s_cntw[i] = 0;
+    // Every chunk load is issued before any is used (a select or a branch
+    // between them would wait for each in turn): clamped in-bounds addresses,
+    // validity applied afterwards, the ragged tail (R % 4 != 0) read last.
+    // No vector read at all when R < 4: it would pass the end of ids.
+    if (R >= 4) {
+#pragma unroll
+      for (int u = 0; u < kIdChunks; ++u) {
+        const int r = (c_begin + u) * 256 + 4 * lane;
+        idv[u] = *reinterpret_cast<const int4*>(p.ids + (r + 3 < R ? r : R - 4));
+      }
+    }
 #pragma unroll
     for (int u = 0; u < kIdChunks; ++u) {
       const int r = (c_begin + u) * 256 + 4 * lane;
-      const bool full = c_begin + u < c_end && r + 3 < R;
-      // (no vector read at all when R < 4: it would pass the end of ids)
-      const int4 v = R >= 4 ? *reinterpret_cast<const int4*>(p.ids + (full ? r : 0))
-                            : make_int4(-1, -1, -1, -1);
-      idv[u] = full ? v : make_int4(-1, -1, -1, -1);
-      if (c_begin + u < c_end && r < R && r + 3 >= R) {  // the ragged tail (R % 4 != 0)
+      const bool full = R >= 4 && c_begin + u < c_end && r + 3 < R;
+      idv[u] = full ? idv[u] : make_int4(-1, -1, -1, -1);
+    }
+#pragma unroll
+    for (int u = 0; u < kIdChunks; ++u) {
+      const int r = (c_begin + u) * 256 + 4 * lane;
+      if (c_begin + u < c_end && r < R && r + 3 >= R) {  // the ragged tail
         idv[u].x = p.ids[r];
         if (r + 1 < R) idv[u].y = p.ids[r + 1];
         if (r + 2 < R) idv[u].z = p.ids[r + 2];
