@@ -258,6 +258,34 @@ def test_histogram_scan_c3(ctx, guarded, experts, dist, routes):
         assert np.array_equal(cnt.read(), e_c)
 
 
+@pytest.mark.parametrize("routes,experts,offset", [(65537, 7, 0), (200003, 1024, 0), (150001, 33, 1),
+                                                   (1 << 20, 2, 0), (70000, 256, 3)])
+def test_histogram_large_paths(ctx, guarded, routes, experts, offset):
+    """Multi-block path (R > 65536): ragged end, unaligned ids (scalar loads),
+    E = 1024 (several passes per block), out-of-range ids skipped, and two calls
+    in a row on the same buffers (the last-block ticket starts from zero each
+    call)."""
+    rng = np.random.default_rng(routes + experts)
+    ids_h = rng.integers(0, experts, routes).astype(np.int32)
+    ids_h[rng.integers(0, routes, 50)] = -3
+    ids_h[rng.integers(0, routes, 50)] = experts + 5
+    valid = ids_h[(ids_h >= 0) & (ids_h < experts)]
+    e_c = np.bincount(valid, minlength=experts).astype(np.int32)
+    e_o = np.concatenate([[0], np.cumsum(e_c)]).astype(np.int32)
+    ids = guarded(routes, np.int32, ids_h, offset_elems=offset)
+    for _ in range(2):
+        counts = guarded(experts, np.int32, np.full(experts, 123, np.int32))
+        offsets = guarded(experts + 1, np.int32, np.full(experts + 1, 456, np.int32))
+        ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
+            expert_ids=ids.ptr, counts=counts.ptr, offsets=offsets.ptr, route_pairs=routes,
+            experts=experts, kernel=NATIVE), ctx))
+        assert np.array_equal(counts.read(), e_c) and np.array_equal(offsets.read(), e_o)
+        ok(rr.histogram(rr.HistogramArgs(expert_ids=ids.ptr, counts=counts.ptr, route_pairs=routes,
+                                         experts=experts, kernel=NATIVE), ctx))
+        assert np.array_equal(counts.read(), e_c)
+        assert counts.canaries_intact() and offsets.canaries_intact() and ids.canaries_intact()
+
+
 # -------------------------------------------------------------------- permute
 
 def run_permute(ctx, device, x_h, ids_h, experts, kernel, with_inverse=True, offset=0):
