@@ -95,6 +95,11 @@ struct TileShape {
 // clamped addresses and zeroing at the LDS store, as the strip kernel does,
 // measured slower here: C4 grouped GEMM 17.1 ms against 15.6 ms, the selects
 // adding VALU work to every k step of an MFMA-bound loop.)
+// 16-byte vector that needs only 4-byte alignment: gfx950 global memory takes
+// unaligned vector accesses, so rows of widths that are not multiples of 4 load
+// whole quads with one instruction.
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
 template <class S, bool VEC>
 struct Stage {
   float a[S::kALoads][4];
@@ -118,6 +123,9 @@ struct Stage {
         } else {
           a[p][0] = a[p][1] = a[p][2] = a[p][3] = 0.0F;
         }
+      } else if (src >= 0 && k + 3 < K) {  // whole quad: one 16-byte load (4-byte aligned)
+        const f4u v = *reinterpret_cast<const f4u*>(ptr);
+        a[p][0] = v.x; a[p][1] = v.y; a[p][2] = v.z; a[p][3] = v.w;
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[p][j] = (src >= 0 && k + j < K) ? ptr[j] : 0.0F;
@@ -138,6 +146,9 @@ struct Stage {
         } else {
           b[p][0] = b[p][1] = b[p][2] = b[p][3] = 0.0F;
         }
+      } else if (k < K && col + 3 < N) {  // whole quad: one 16-byte load (4-byte aligned)
+        const f4u v = *reinterpret_cast<const f4u*>(ptr);
+        b[p][0] = v.x; b[p][1] = v.y; b[p][2] = v.z; b[p][3] = v.w;
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) b[p][j] = (k < K && col + j < N) ? ptr[j] : 0.0F;
@@ -180,6 +191,8 @@ struct Stage {
       float* ptr = out + static_cast<std::size_t>(row0 + r) * K + k;
       if (VEC) {
         if (k < K) *reinterpret_cast<float4*>(ptr) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
+      } else if (k + 3 < K) {
+        *reinterpret_cast<f4u*>(ptr) = f4u{a[p][0], a[p][1], a[p][2], a[p][3]};
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

@@ -535,31 +535,44 @@ __global__ __launch_bounds__(WAVES * 64) void rr_route_prep_kernel(
 
 // Token-owned row copy: element (t, c) of x is read once and stored to every
 // valid destination row of token t. VEC4: c indexes float4 columns.
-template <bool VEC4>
+// Quad items: item (t, c) moves elements [4c, 4c + 4) of a row with one
+// 16-byte access that needs only 4-byte alignment (gfx950 global memory takes
+// unaligned vector accesses), and the last 1-3 elements of a row whose width
+// is not a multiple of 4 element by element. Rows of any width and offset
+// stay on vector loads and stores.
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ uint32_t quads_of(int width) { return (static_cast<uint32_t>(width) + 3u) / 4u; }
+
 __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __restrict__ x,
                                                               const int32_t* __restrict__ route_pos,
                                                               float* __restrict__ x_permuted,
                                                               int tokens, int top_k, int hidden,
                                                               int routes) {
-  const uint32_t cols = VEC4 ? static_cast<uint32_t>(hidden) / 4 : static_cast<uint32_t>(hidden);
+  const uint32_t cols = quads_of(hidden);
   const uint32_t total = static_cast<uint32_t>(tokens) * cols;
   const uint32_t stride = blockDim.x * gridDim.x;
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const uint32_t t = i / cols;
     const uint32_t c = i - t * cols;
-    if (VEC4) {
-      const float4 v = reinterpret_cast<const float4*>(x + static_cast<std::size_t>(t) * hidden)[c];
+    const int k0 = static_cast<int>(4 * c);
+    const float* src = x + static_cast<std::size_t>(t) * hidden + k0;
+    if (k0 + 4 <= hidden) {
+      const f4u v = *reinterpret_cast<const f4u*>(src);
       for (int j = 0; j < top_k; ++j) {
         const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
         if (pos >= 0 && pos < routes) {
-          reinterpret_cast<float4*>(x_permuted + static_cast<std::size_t>(pos) * hidden)[c] = v;
+          *reinterpret_cast<f4u*>(x_permuted + static_cast<std::size_t>(pos) * hidden + k0) = v;
         }
       }
     } else {
-      const float v = x[static_cast<std::size_t>(t) * hidden + c];
+      const int n = hidden - k0;  // 1..3
       for (int j = 0; j < top_k; ++j) {
         const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
-        if (pos >= 0 && pos < routes) x_permuted[static_cast<std::size_t>(pos) * hidden + c] = v;
+        if (pos >= 0 && pos < routes) {
+          float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden + k0;
+          for (int q = 0; q < n; ++q) dst[q] = src[q];
+        }
       }
     }
   }
@@ -571,44 +584,46 @@ __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __res
 // operation order of the reference's FP32 loop (reference
 // benchmarks/adapters/unpermute_adapter.cpp:67-73).
 // ============================================================================
-template <bool VEC4>
 __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restrict__ y_permuted,
                                                            const int32_t* __restrict__ route_pos,
                                                            const float* __restrict__ route_weights,
                                                            float* __restrict__ y, int tokens,
                                                            int top_k, int output) {
-  const uint32_t cols = VEC4 ? static_cast<uint32_t>(output) / 4 : static_cast<uint32_t>(output);
+  const uint32_t cols = quads_of(output);
   const uint32_t total = static_cast<uint32_t>(tokens) * cols;
   const uint32_t stride = blockDim.x * gridDim.x;
   const int routes = tokens * top_k;
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const uint32_t t = i / cols;
     const uint32_t c = i - t * cols;
-    if (VEC4) {
-      float4 acc = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+    const int k0 = static_cast<int>(4 * c);
+    float* out = y + static_cast<std::size_t>(t) * output + k0;
+    if (k0 + 4 <= output) {
+      f4u acc = f4u{0.0F, 0.0F, 0.0F, 0.0F};
       for (int j = 0; j < top_k; ++j) {
         const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
         const int32_t pos = route_pos[route];
         if (pos < 0 || pos >= routes) continue;
         const float w = route_weights[route];
-        const float4 v =
-            reinterpret_cast<const float4*>(y_permuted + static_cast<std::size_t>(pos) * output)[c];
+        const f4u v = *reinterpret_cast<const f4u*>(y_permuted + static_cast<std::size_t>(pos) * output + k0);
         acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
         acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
         acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
         acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
       }
-      reinterpret_cast<float4*>(y + static_cast<std::size_t>(t) * output)[c] = acc;
+      *reinterpret_cast<f4u*>(out) = acc;
     } else {
-      float acc = 0.0F;
+      const int n = output - k0;  // 1..3
+      float acc[3] = {0.0F, 0.0F, 0.0F};
       for (int j = 0; j < top_k; ++j) {
         const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
         const int32_t pos = route_pos[route];
         if (pos < 0 || pos >= routes) continue;
-        acc = __fadd_rn(acc, __fmul_rn(route_weights[route],
-                                       y_permuted[static_cast<std::size_t>(pos) * output + c]));
+        const float w = route_weights[route];
+        const float* v = y_permuted + static_cast<std::size_t>(pos) * output + k0;
+        for (int q = 0; q < n; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(w, v[q]));
       }
-      y[static_cast<std::size_t>(t) * output + c] = acc;
+      for (int q = 0; q < n; ++q) out[q] = acc[q];
     }
   }
 }
@@ -697,16 +712,10 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || hidden == 0) return err;
-  const bool vec4 = (hidden % 4 == 0) && aligned16(x) && aligned16(x_permuted);
-  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? hidden / 4 : hidden);
+  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(hidden) + 3) / 4);
   if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  if (vec4) {
-    rr_permute_copy_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
-        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
-  } else {
-    rr_permute_copy_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
-        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
-  }
+  rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
+                                                                 top_k, hidden, routes);
   return hipGetLastError();
 }
 
@@ -737,16 +746,10 @@ hipError_t permute_copy(const float* x, const int32_t* route_pos, float* x_permu
                         int top_k, int hidden, hipStream_t stream) {
   const int routes = tokens * top_k;
   if (routes <= 0 || hidden <= 0) return hipSuccess;
-  const bool vec4 = (hidden % 4 == 0) && aligned16(x) && aligned16(x_permuted);
-  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? hidden / 4 : hidden);
+  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(hidden) + 3) / 4);
   if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  if (vec4) {
-    rr_permute_copy_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
-        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
-  } else {
-    rr_permute_copy_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
-        x, route_pos, x_permuted, tokens, top_k, hidden, routes);
-  }
+  rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
+                                                                 top_k, hidden, routes);
   return hipGetLastError();
 }
 
@@ -754,16 +757,10 @@ hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
                             const float* route_weights, float* y, int tokens, int top_k,
                             int output, hipStream_t stream) {
   if (tokens <= 0 || output <= 0) return hipSuccess;
-  const bool vec4 = (output % 4 == 0) && aligned16(y_permuted) && aligned16(y);
-  const uint64_t items = static_cast<uint64_t>(tokens) * (vec4 ? output / 4 : output);
+  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(output) + 3) / 4);
   if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  if (vec4) {
-    rr_unpermute_kernel<true><<<stream_grid(items), 256, 0, stream>>>(
-        y_permuted, route_pos, route_weights, y, tokens, top_k, output);
-  } else {
-    rr_unpermute_kernel<false><<<stream_grid(items), 256, 0, stream>>>(
-        y_permuted, route_pos, route_weights, y, tokens, top_k, output);
-  }
+  rr_unpermute_kernel<<<stream_grid(items), 256, 0, stream>>>(y_permuted, route_pos, route_weights,
+                                                              y, tokens, top_k, output);
   return hipGetLastError();
 }
 
