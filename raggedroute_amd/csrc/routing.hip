@@ -542,8 +542,12 @@ __global__ __launch_bounds__(WAVES * 64) void rr_route_prep_kernel(
 // stay on vector loads and stores.
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 
-__device__ __forceinline__ uint32_t quads_of(int width) { return (static_cast<uint32_t>(width) + 3u) / 4u; }
+__host__ __device__ inline uint32_t quads_of(int width) { return (static_cast<uint32_t>(width) + 3u) / 4u; }
 
+// Narrow rows (under 1024 floats): one thread per (token, quad) item, items
+// in token-major order, grid-stride. A wave per token would leave most lanes
+// idle here (the 128-float rows of the headline unpermute ran at 6.4 us that
+// way, 4.0 us with items).
 __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __restrict__ x,
                                                               const int32_t* __restrict__ route_pos,
                                                               float* __restrict__ x_permuted,
@@ -578,12 +582,6 @@ __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __res
   }
 }
 
-// ============================================================================
-// Unpermute: y[t, :] = sum_j w[t*top_k + j] * y_permuted[route_pos[t*top_k + j], :]
-// accumulated in rank order with separately rounded multiply and add, the
-// operation order of the reference's FP32 loop (reference
-// benchmarks/adapters/unpermute_adapter.cpp:67-73).
-// ============================================================================
 __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restrict__ y_permuted,
                                                            const int32_t* __restrict__ route_pos,
                                                            const float* __restrict__ route_weights,
@@ -628,10 +626,181 @@ __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restri
   }
 }
 
+// Token-owned rows: wave w of the grid copies rows t = w, w + waves, ...;
+// lane j reads route j's position once per row (routes beyond the first 64 of
+// a row, possible only in the stand-alone permute, are read 64 at a time),
+// then the lanes stride over the row's quads, eight in flight per lane (x read
+// once, written top_k times). Output rows go out with nontemporal stores: they
+// are not read again by the kernel, and streaming them past the caches cut
+// the C4 copy (T = 8192, 16 KB rows) from 89 to 69 us.
+constexpr int kRowQuadsInFlight = 8;
+
+__global__ __launch_bounds__(256) void rr_permute_rows_kernel(const float* __restrict__ x,
+                                                              const int32_t* __restrict__ route_pos,
+                                                              float* __restrict__ x_permuted,
+                                                              int tokens, int top_k, int hidden,
+                                                              int routes) {
+  const int lane = lane_id();
+  const int cols = static_cast<int>(quads_of(hidden));
+  const int waves = static_cast<int>(gridDim.x) * 4;
+  for (int t = static_cast<int>(blockIdx.x) * 4 + (static_cast<int>(threadIdx.x) >> 6); t < tokens;
+       t += waves) {
+    const int32_t* row_pos = route_pos + static_cast<std::size_t>(t) * top_k;
+    const int32_t pos0 = lane < top_k ? row_pos[lane] : -1;
+    const float* src = x + static_cast<std::size_t>(t) * hidden;
+    for (int q0 = 0; q0 < cols; q0 += 64 * kRowQuadsInFlight) {  // wave-uniform: readlane needs every lane
+      f4u v[kRowQuadsInFlight];
+#pragma unroll
+      for (int u = 0; u < kRowQuadsInFlight; ++u) {
+        const int k0 = 4 * (q0 + lane + 64 * u);
+        if (k0 + 4 <= hidden) {
+          v[u] = *reinterpret_cast<const f4u*>(src + k0);
+        } else {
+          v[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
+          for (int e = 0; k0 + e < hidden; ++e) v[u][e] = src[k0 + e];
+        }
+      }
+      for (int j0 = 0; j0 < top_k; j0 += 64) {
+        const int32_t my_pos = j0 == 0 ? pos0 : (j0 + lane < top_k ? row_pos[j0 + lane] : -1);
+        const int n = min(64, top_k - j0);
+        for (int j = 0; j < n; ++j) {
+          const int32_t pos = __builtin_amdgcn_readlane(my_pos, j);
+          if (pos < 0 || pos >= routes) continue;  // wave-uniform
+          float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden;
+#pragma unroll
+          for (int u = 0; u < kRowQuadsInFlight; ++u) {
+            const int k0 = 4 * (q0 + lane + 64 * u);
+            if (k0 + 4 <= hidden) {
+              __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(dst + k0));
+            } else {
+              for (int e = 0; k0 + e < hidden; ++e) dst[k0 + e] = v[u][e];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ============================================================================
+// Unpermute: y[t, :] = sum_j w[t*top_k + j] * y_permuted[route_pos[t*top_k + j], :]
+// accumulated in rank order with separately rounded multiply and add, the
+// operation order of the reference's FP32 loop (reference
+// benchmarks/adapters/unpermute_adapter.cpp:67-73).
+// ============================================================================
+__global__ __launch_bounds__(256) void rr_unpermute_rows_kernel(const float* __restrict__ y_permuted,
+                                                           const int32_t* __restrict__ route_pos,
+                                                           const float* __restrict__ route_weights,
+                                                           float* __restrict__ y, int tokens,
+                                                           int top_k, int output) {
+  // Token-owned rows as in the permute copy: lane j < top_k reads route j's
+  // position and weight once per row. y_permuted rows are read once, with
+  // nontemporal loads (C4 unpermute 265 -> 255 us).
+  const int lane = lane_id();
+  const int cols = static_cast<int>(quads_of(output));
+  const int waves = static_cast<int>(gridDim.x) * 4;
+  const int routes = tokens * top_k;
+  for (int t = static_cast<int>(blockIdx.x) * 4 + (static_cast<int>(threadIdx.x) >> 6); t < tokens;
+       t += waves) {
+    const std::size_t r0 = static_cast<std::size_t>(t) * top_k;
+    const int32_t my_pos = lane < top_k ? route_pos[r0 + lane] : -1;
+    const float my_w = lane < top_k ? route_weights[r0 + lane] : 0.0F;
+    float* out = y + static_cast<std::size_t>(t) * output;
+    for (int q0 = 0; q0 < cols; q0 += 64 * kRowQuadsInFlight) {  // wave-uniform: readlane needs every lane
+      f4u acc[kRowQuadsInFlight];
+#pragma unroll
+      for (int u = 0; u < kRowQuadsInFlight; ++u) acc[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
+      for (int j = 0; j < top_k; j += 2) {  // two routes' loads in flight, summed in rank order
+        const int32_t p0 = __builtin_amdgcn_readlane(my_pos, j);
+        const int32_t p1 = j + 1 < top_k ? __builtin_amdgcn_readlane(my_pos, j + 1) : -1;
+        const bool ok0 = p0 >= 0 && p0 < routes;  // wave-uniform
+        const bool ok1 = p1 >= 0 && p1 < routes;
+        const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+        const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j + 1 < top_k ? j + 1 : j));
+        // An invalid position reads row 0 (present: routes > 0) and is not summed.
+        const float* s0 = y_permuted + static_cast<std::size_t>(ok0 ? p0 : 0) * output;
+        const float* s1 = y_permuted + static_cast<std::size_t>(ok1 ? p1 : 0) * output;
+        f4u v0[kRowQuadsInFlight], v1[kRowQuadsInFlight];
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) {
+          const int k0 = 4 * (q0 + lane + 64 * u);
+          if (k0 + 4 <= output) {
+            v0[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(s0 + k0));
+            v1[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(s1 + k0));
+          } else {
+            v0[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
+            v1[u] = v0[u];
+            for (int e = 0; k0 + e < output; ++e) {
+              v0[u][e] = s0[k0 + e];
+              v1[u][e] = s1[k0 + e];
+            }
+          }
+        }
+        if (ok0) {
+#pragma unroll
+          for (int u = 0; u < kRowQuadsInFlight; ++u) {
+            acc[u].x = __fadd_rn(acc[u].x, __fmul_rn(w0, v0[u].x));
+            acc[u].y = __fadd_rn(acc[u].y, __fmul_rn(w0, v0[u].y));
+            acc[u].z = __fadd_rn(acc[u].z, __fmul_rn(w0, v0[u].z));
+            acc[u].w = __fadd_rn(acc[u].w, __fmul_rn(w0, v0[u].w));
+          }
+        }
+        if (ok1) {
+#pragma unroll
+          for (int u = 0; u < kRowQuadsInFlight; ++u) {
+            acc[u].x = __fadd_rn(acc[u].x, __fmul_rn(w1, v1[u].x));
+            acc[u].y = __fadd_rn(acc[u].y, __fmul_rn(w1, v1[u].y));
+            acc[u].z = __fadd_rn(acc[u].z, __fmul_rn(w1, v1[u].z));
+            acc[u].w = __fadd_rn(acc[u].w, __fmul_rn(w1, v1[u].w));
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRowQuadsInFlight; ++u) {
+        const int k0 = 4 * (q0 + lane + 64 * u);
+        if (k0 + 4 <= output) {
+          __builtin_nontemporal_store(acc[u], reinterpret_cast<f4u*>(out + k0));
+        } else {
+          for (int e = 0; k0 + e < output; ++e) out[k0 + e] = acc[u][e];
+        }
+      }
+    }
+  }
+}
+
+// Row kernels index a row's floats with int (quad offsets run up to 1024 past the width).
+constexpr int kMaxRowWidth = INT_MAX - 4096;
+
+// Row width (floats) from which the token-owned row kernels are used.
+constexpr int kWideRow = 1024;
+
 unsigned stream_grid(uint64_t items) {
   // Enough blocks to cover 256 CUs several times; grid-stride beyond that.
   const uint64_t blocks = (items + 255) / 256;
   return static_cast<unsigned>(blocks < 8192 ? (blocks == 0 ? 1 : blocks) : 8192);
+}
+
+unsigned row_grid(int rows) {
+  // One wave per row, four waves per block, one block per CU, grid-stride
+  // beyond that (C4 unpermute, 57 KB rows: 324 us with 128 blocks, 264 with
+  // 256, 271 with 512, 272 with one wave per token).
+  const int blocks = (rows + 3) / 4;
+  return static_cast<unsigned>(blocks < 256 ? (blocks == 0 ? 1 : blocks) : 256);
+}
+
+hipError_t launch_permute_copy(const float* x, const int32_t* route_pos, float* x_permuted,
+                               int tokens, int top_k, int hidden, int routes, hipStream_t stream) {
+  if (hidden >= kWideRow) {
+    if (hidden > kMaxRowWidth) return hipErrorInvalidValue;
+    rr_permute_rows_kernel<<<row_grid(tokens), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
+                                                                 top_k, hidden, routes);
+  } else {
+    const uint64_t items = static_cast<uint64_t>(tokens) * quads_of(hidden);
+    if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;  // 32-bit item indices
+    rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
+                                                                   top_k, hidden, routes);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -712,11 +881,7 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || hidden == 0) return err;
-  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(hidden) + 3) / 4);
-  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
-                                                                 top_k, hidden, routes);
-  return hipGetLastError();
+  return launch_permute_copy(x, route_pos, x_permuted, tokens, top_k, hidden, routes, stream);
 }
 
 hipError_t route_prep(const int32_t* ids, int32_t* counts, int32_t* offsets, int32_t* cursors,
@@ -746,21 +911,24 @@ hipError_t permute_copy(const float* x, const int32_t* route_pos, float* x_permu
                         int top_k, int hidden, hipStream_t stream) {
   const int routes = tokens * top_k;
   if (routes <= 0 || hidden <= 0) return hipSuccess;
-  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(hidden) + 3) / 4);
-  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
-                                                                 top_k, hidden, routes);
-  return hipGetLastError();
+  return launch_permute_copy(x, route_pos, x_permuted, tokens, top_k, hidden, routes, stream);
 }
 
 hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
                             const float* route_weights, float* y, int tokens, int top_k,
                             int output, hipStream_t stream) {
   if (tokens <= 0 || output <= 0) return hipSuccess;
-  const uint64_t items = static_cast<uint64_t>(tokens) * ((static_cast<uint64_t>(output) + 3) / 4);
-  if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;
-  rr_unpermute_kernel<<<stream_grid(items), 256, 0, stream>>>(y_permuted, route_pos, route_weights,
-                                                              y, tokens, top_k, output);
+  if (output >= kWideRow) {
+    if (output > kMaxRowWidth) return hipErrorInvalidValue;
+    rr_unpermute_rows_kernel<<<row_grid(tokens), 256, 0, stream>>>(y_permuted, route_pos,
+                                                                   route_weights, y, tokens, top_k,
+                                                                   output);
+  } else {
+    const uint64_t items = static_cast<uint64_t>(tokens) * quads_of(output);
+    if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;  // 32-bit item indices
+    rr_unpermute_kernel<<<stream_grid(items), 256, 0, stream>>>(y_permuted, route_pos, route_weights,
+                                                                y, tokens, top_k, output);
+  }
   return hipGetLastError();
 }
 

@@ -337,6 +337,10 @@ def test_permute_unaligned_duplicate_ids(ctx, device, kat, kernel):
 @pytest.mark.parametrize("tokens,experts,top_k,hidden", [
     (5, 4, 2, 7), (512, 32, 2, 256), (4096, 64, 2, 256), (1000, 8, 1, 33), (777, 16, 4, 64),
     (3000, 1024, 2, 12), (20000, 128, 2, 4), (300, 600, 8, 20), (64, 4, 2, 0),
+    # token-owned row kernel (rows of 1024 floats or more): rows wider than one
+    # pass of a wave (2048 floats) with a 3-float tail, more than 64 routes per
+    # token (position lanes read in chunks of 64); item kernel with many routes
+    (50, 8, 2, 2051), (20, 200, 100, 1500), (9, 16, 3, 1024), (40, 200, 130, 9), (17, 1024, 1024, 5),
 ])
 def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     rng = np.random.default_rng(tokens + experts)
@@ -489,7 +493,8 @@ def run_unpermute(ctx, device, yp_h, pos_h, w_h, top_k, kernel, offset=0):
 
 
 @pytest.mark.parametrize("tokens,top_k,output", [(5, 2, 5), (4096, 2, 128), (1000, 1, 33), (333, 8, 64),
-                                                 (8192, 2, 1433), (2048, 4, 4)])
+                                                 (8192, 2, 1433), (2048, 4, 4), (64, 64, 1030),
+                                                 (3, 63, 4097), (7, 3, 1024), (6, 2, 1023)])
 def test_unpermute_bit_exact(ctx, device, tokens, top_k, output):
     rng = np.random.default_rng(tokens + output)
     yp = rng.standard_normal((tokens * top_k, output)).astype(np.float32)
