@@ -305,13 +305,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 8 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
+  // chain: [max_strips * 16] token of each slot's route (-1: none), [max_strips][4] strip info
+  int32_t* s_tok = reinterpret_cast<int32_t*>(s_w + (MODE == kStripChain ? p.max_strips * kRows : 0));
+  int32_t* s_info = s_tok + (MODE == kStripChain ? p.max_strips * kRows : 0);
   // chain: [waves][64 nblk] route-id histogram of each wave's chunks
-  int32_t* s_cntw = reinterpret_cast<int32_t*>(s_w + (MODE == kStripChain ? p.max_strips * kRows : 0));
+  int32_t* s_cntw = s_info + (MODE == kStripChain ? p.max_strips * 4 : 0);
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int wave = tid >> 6;
-  const int g = lane >> 4;
+  const int g = (lane >> 4) & 3;  // (the mask tells the compiler g < 4)
   const int li = lane & 15;
   const int grid = static_cast<int>(gridDim.x);
   const int b = static_cast<int>(blockIdx.x);
@@ -368,6 +371,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     c_begin = wave * nchunks / kWaves;
     c_end = (wave + 1) * nchunks / kWaves;
     for (int i = tid; i < kWaves * 64 * nblk; i += kThreads) s_cntw[i] = 0;
+    // Empty route slots of every strip this workgroup may own: cleared here,
+    // barriers before the rank passes, whose waves fill slots that another
+    // wave's thread would otherwise clear (a clear racing a fill loses the route).
+    for (int i = tid; i < p.max_strips * kRows; i += kThreads) s_slot[i] = -1;
     // Every chunk load is issued before any is used (a select or a branch
     // between them would wait for each in turn): clamped in-bounds addresses,
     // validity applied afterwards, the ragged tail (R % 4 != 0) read last.
@@ -480,12 +487,30 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     cur = info(s0);
     if constexpr (MODE == kStripGrouped) load_b(cur.e);  // in flight below
   }
+  if constexpr (MODE == kStripChain) {
+    // Every strip's info, once and in parallel (wave w: strips s0 + w,
+    // s0 + w + waves, ...), for the strip loop to read back from LDS (read
+    // after the barrier that ends the rank passes).
+#pragma unroll 1
+    for (int k = wave; k < s1 - s0; k += kWaves) {
+      const StripInfo si = strip_info(tab, nblk, E, s0 + k);
+      if (lane == 0) *reinterpret_cast<int4*>(s_info + 4 * k) = make_int4(si.e, si.row0, si.row_end, si.rank0);
+    }
+  }
+  auto next_info = [&](int s) -> StripInfo {
+    if constexpr (MODE == kStripChain) {
+      const int4 v = *reinterpret_cast<const int4*>(s_info + 4 * (s - s0));
+      return StripInfo{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                       __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+    } else {
+      return info(s);
+    }
+  };
 
   // ------------------------------------------- chain: routes of my strips
   float w_pending = 0.0F;
   if constexpr (MODE == kStripChain) {
     const int slots = (s1 - s0) * kRows;
-    for (int i = tid; i < slots; i += kThreads) s_slot[i] = -1;
     // My segments: segment e covers my strips [s, last), i.e. its stable
     // ranks [lo, hi), stored from slot base + rank. The walk (ballot lookups
     // and readlanes, uniform control flow only) runs once per wave into the
@@ -570,6 +595,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     }
     if (tid < slots) {  // slots <= (kMaxSegs + 1) * 16 <= kThreads
       const int32_t route = s_slot[tid];
+      s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
       if (route >= 0) {
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
@@ -586,8 +612,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   auto a_source = [&](int s, const StripInfo& si) -> int {
     if constexpr (MODE == kStripChain) {
       (void)si;
-      const int32_t route = s_slot[(s - s0) * kRows + a_row];
-      return route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
+      if (s == s0) {  // before the loop: s_tok is written after the last barrier
+        const int32_t route = s_slot[a_row];
+        return route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
+      }
+      return s_tok[(s - s0) * kRows + a_row];
     } else {
       (void)s;
       const int row = si.row0 + a_row;
@@ -604,13 +633,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     }
   };
 
+  // chain: route and weight of the deferred strip's rows 4g + r, read from LDS
+  // when the strip is deferred (not between the next strip's MFMAs)
+  int32_t ep_route[4] = {-1, -1, -1, -1};
+  float ep_w[4] = {0.0F, 0.0F, 0.0F, 0.0F};
   // ---- epilogue of one output row group: acc[t][r] is row 4g + r, column
   // col0 + 16 t ----
   const int col0 = 16 * kTiles * wave + li;
   auto epilogue_row = [&](int r, const v4f (&a)[kTiles], const StripInfo& st) {
     const int rl = 4 * g + r;
     if constexpr (MODE == kStripChain) {
-      const int32_t route = s_slot[st.rank0 + rl];  // st.rank0: slot of the strip's row 0
+      const int32_t route = ep_route[r];
       if (route >= 0) {
         float* crow = p.C + static_cast<std::size_t>(st.row0 + rl) * N;
 #pragma unroll
@@ -621,7 +654,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if (p.combine) {
           // Both routes of a token add into the zeroed output: fl(0 + a) + b
           // is the same in either order, so the combine is deterministic.
-          const float w = s_w[st.rank0 + rl];
+          const float w = ep_w[r];
           float* yrow = p.y + static_cast<std::size_t>(route >> 1) * N;
 #pragma unroll
           for (int t = 0; t < kTiles; ++t) {
@@ -686,7 +719,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     __syncthreads();
     // ---- prefetch the next strip's A rows (and B of its segment) ----
     if (s + 1 < s1) {
-      cur = info(s + 1);
+      cur = next_info(s + 1);
       src = a_source(s + 1, cur);
       load_a(src);
       if (cur.e != si.e) load_b(cur.e);
@@ -702,13 +735,29 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
     const float* aw = As + li * kLd + 4 * g;
     const float* bw = Bs + (16 * kTiles * wave + li) * kLd + 4 * g;
+    // Software pipelined: chunk c + 1's operands are read from LDS before
+    // chunk c's MFMAs issue, so their latency hides behind that chunk's
+    // dependent MFMA chain (k order unchanged).
+    v4f af_next = *reinterpret_cast<const v4f*>(aw);
+    v4f bf_next[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) bf_next[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd);
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
       if (c < chunks) {
-        const v4f af = *reinterpret_cast<const v4f*>(aw + 16 * c);
+        const v4f af = af_next;
         v4f bf[kTiles];
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) bf[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd + 16 * c);
+        for (int t = 0; t < kTiles; ++t) bf[t] = bf_next[t];
+        if (c + 1 < chunks) {
+          af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t) {
+            bf_next[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd + 16 * (c + 1));
+          }
+        }
+        // (the scheduler would otherwise sink those reads to their use)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[t].x, acc[t], 0, 0, 0);
 #pragma unroll
@@ -717,6 +766,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[t].z, acc[t], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[t].w, acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (kDeferred) {
         if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
@@ -729,6 +779,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       for (int t = 0; t < kTiles; ++t) acc_prev[t] = acc[t];
       prev = si;
       prev.rank0 = (s - s0) * kRows;  // slot of the strip's first row (chain)
+      if constexpr (MODE == kStripChain) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ep_route[r] = s_slot[prev.rank0 + 4 * g + r];
+          ep_w[r] = s_w[prev.rank0 + 4 * g + r];
+        }
+      }
       pending = true;
     } else {
 #pragma unroll
@@ -828,7 +885,8 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   bytes += kMaxBlocks * 64 * sizeof(int32_t);
   if (mode == kStripChain) {
     bytes += static_cast<std::size_t>(waves) * kMaxSegs * 8 * sizeof(int32_t);  // segment lists
-    bytes += 2 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);
+    bytes += 3 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);  // slots, weights, tokens
+    bytes += static_cast<std::size_t>(max_strips) * 4 * sizeof(int32_t);          // strip info
     bytes += static_cast<std::size_t>(waves) * 64 * ((segments + 63) / 64) * sizeof(int32_t);  // per-wave histograms
   }
   return bytes;

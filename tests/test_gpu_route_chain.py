@@ -223,3 +223,23 @@ def test_fused_route_chain_matches_stage_by_stage(ctx, device, shape, with_x_per
     for key, a in fused.items():
         assert _same(a, ref[key]), f"{key} differs"
     check_route_chain(cfg, inp, fused)
+
+
+@pytest.mark.parametrize("shape", [(512, 64, 2, 128, 128), (2048, 32, 4, 64, 64), (1000, 7, 3, 40, 24)])
+def test_route_chain_repeats_bit_for_bit(ctx, device, shape):
+    """Several calls on one set of buffers, every output poisoned before each:
+    a slot, row or map entry that a call fails to write shows up as NaN or -7
+    instead of passing on the previous call's value."""
+    t, e, top, k, n = shape
+    cfg = workloads.RouteChainConfig("repeat", t, e, k, n, top, "zipf")
+    inp = workloads.route_chain_inputs(cfg, seed=11)
+    run = RouteChainRun(cfg, inp, device)
+    first = run.run(ctx)
+    check_route_chain(cfg, inp, first)
+    for _ in range(3):
+        for attr in ("counts", "offsets", "xp", "pos", "inv", "yp", "y"):
+            getattr(run, attr).fill_(float("nan") if getattr(run, attr).dtype == torch.float32 else -7)
+        again = run.run(ctx)
+        for key, v in first.items():
+            a, b = (again[key].view(np.uint32), v.view(np.uint32)) if v.dtype == np.float32 else (again[key], v)
+            assert np.array_equal(a, b), key
