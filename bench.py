@@ -336,7 +336,7 @@ def headline(torch, device, args):
                              "launches": launches, "stages": stages, "active_experts": active}
 
 
-def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50):
+def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50, cpu_sample=False):
     """Mixtral-shaped ragged grouped GEMM + permute + unpermute: T=8192, R=16384,
     E=8 with 7 active (Zipf 1.2), expert 7 empty."""
     import raggedroute_amd as rr
@@ -364,12 +364,14 @@ def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50):
         nbytes, flops = model[name]
         out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
     out["permute_gbs_reference_model"] = round(2 * 4 * 2 * t * hidden / (out["token_permute"]["us"] * 1e-6) / 1e9, 1)
+    if cpu_sample:
+        out["cpu_sample"] = cpu_sample_c4(ch, we, 2 * t)
     del ch, x, we
     torch.cuda.empty_cache()
     return out
 
 
-def c5(torch, device, steps=20):
+def c5(torch, device, steps=20, cpu_sample=False):
     from raggedroute_amd import workloads
     cfg = workloads.C5
     inputs = workloads.chain_inputs_device(cfg, 0, device)
@@ -380,10 +382,58 @@ def c5(torch, device, steps=20):
                              fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, ch, 10, model)
+    out = {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1),
+           "launches": launches, "stages": stages}
+    if cpu_sample:
+        out["cpu_sample"] = cpu_sample_c5(inputs, cfg)
     del ch, inputs
     torch.cuda.empty_cache()
-    return {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1),
-            "launches": launches, "stages": stages}
+    return out
+
+
+def cpu_sample_c4(ch, expert_weights, routes, rows=8):
+    """C4 grouped GEMM on the oracle (single thread) over `rows` rows of
+    x_permuted spread evenly over its R rows (the full 1.9 TFLOP is out of
+    reach on one core), extrapolated linearly to all R rows."""
+    import oracle
+    offsets = ch.offsets.cpu().numpy().astype(np.int64)
+    pick = np.linspace(0, routes - 1, rows).astype(np.int64)
+    xs = ch.xp[torch_index(pick, ch.xp.device)].cpu().numpy()
+    expert = np.searchsorted(offsets, pick, side="right") - 1
+    offs = np.searchsorted(expert, np.arange(len(offsets)), side="left").astype(np.int32)
+    w = expert_weights.cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.grouped_gemm_f32_seq(xs, w, offs)
+    sec = time.perf_counter() - t0
+    flops = 2.0 * rows * w.shape[1] * w.shape[2]
+    return {"kind": "port", "cores": 1,
+            "sample": f"{rows} of {routes} x_permuted rows (evenly spaced) through the oracle grouped GEMM "
+                      "(single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
+            "sample_ms": round(sec * 1e3, 3), "gflops": round(flops / sec / 1e9, 3),
+            "extrapolated_grouped_gemm_ms": round(sec * routes / rows * 1e3, 1)}
+
+
+def cpu_sample_c5(inputs, cfg, frac=100):
+    """C5 chain_from_tokens on the oracle (single thread) over the first 1 % of
+    the tokens (the full chain is 112 GFLOP scalar), extrapolated linearly."""
+    import oracle
+    n = max(1, cfg.tokens // frac)
+    x = inputs["x"][:n].cpu().numpy()
+    rw = inputs["router_weights"].cpu().numpy()
+    we = inputs["expert_weights"].cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.chain(x, we, router_weights=rw)
+    sec = time.perf_counter() - t0
+    return {"kind": "port", "cores": 1,
+            "sample": f"first {n} of {cfg.tokens} tokens through the oracle chain_from_tokens "
+                      "(single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
+            "sample_ms": round(sec * 1e3, 3), "tokens_per_s": round(n / sec, 1),
+            "extrapolated_chain_ms": round(sec * cfg.tokens / n * 1e3, 1)}
+
+
+def torch_index(idx, device):
+    import torch
+    return torch.from_numpy(np.asarray(idx, np.int64)).to(device)
 
 
 def small_chain(torch, device, cfg, reps=200):
@@ -611,11 +661,11 @@ def main() -> int:
         if "c2" in only:
             extras["C2"] = small_chain(torch, device, workloads.C2)
         if "c4" in only:
-            extras["C4"] = c4(torch, device)
+            extras["C4"] = c4(torch, device, cpu_sample=not args.quick)
         if "c4u" in only:
             extras["C4_nonaligned"] = c4(torch, device, 4095, 14335, reps=3)
         if "c5" in only:
-            extras["C5"] = c5(torch, device)
+            extras["C5"] = c5(torch, device, cpu_sample=not args.quick)
         if "c3" in only:
             extras["C3"] = c3(torch, device)
         if "route" in only:
@@ -635,6 +685,9 @@ def main() -> int:
             sec_c = cpu_chain_seconds(workloads.chain_inputs(c, 0), c.from_tokens)
             others[c.name] = {"tokens_per_s": round(c.tokens / sec_c, 1), "chain_ms": round(sec_c * 1e3, 3),
                               "entry": "chain_from_tokens" if c.from_tokens else "chain_from_logits"}
+        for name in ("C4", "C5"):  # row / token samples taken while their inputs were on the device
+            if name in extras and "cpu_sample" in extras[name]:
+                others[name] = extras[name].pop("cpu_sample")
         cpu = {"value": round(cfg.tokens / sec, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"full headline chain_from_tokens (T={cfg.tokens}, E={cfg.experts}, K={cfg.hidden}, "
                          f"N={cfg.output}) on the oracle/ C restatement of the reference CPU chain "
