@@ -299,9 +299,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   const int kLd = chunks * 16 + 4;
   float* Bs = lds;                // [BN][kLd]: B of the current segment, k contiguous
   float* As = Bs + BN * kLd;      // [16][kLd]: A rows of the current strip
-  uint64_t* s_keys = reinterpret_cast<uint64_t*>(As + kRows * kLd);  // router: [waves][16][2]
-  int32_t* s_cnt =
-      reinterpret_cast<int32_t*>(s_keys + (MODE == kStripRouterGate ? kWaves * kRows * 2 : 0));
+  constexpr int kLgLd = BN + 4;       // router: padded row of the logit tile
+  float* s_lg = As + kRows * kLd;      // router: [16][kLgLd] logits of the strip
+  int32_t* s_cnt = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
   int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 8 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
@@ -792,32 +792,32 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       for (int r = 0; r < 4; ++r) epilogue_row(r, acc, si);
     }
     if constexpr (MODE == kStripRouterGate) {
-      // Top-2 of each row over its N logits: per wave over its 16 columns
-      // (the 16 lanes of a DPP row hold one output row), then over the waves
-      // through LDS.
+      // Top-2 of each row over its N logits: the strip's 16 x BN logits go
+      // through LDS, then the kThreads / 16 lanes of a row each take four
+      // adjacent columns (one ds_read_b128) and merge with register moves.
+      // Keys carry the expert id, so the merge order does not change the pick.
+      constexpr int kRowLanes = kThreads / kRows;  // 16 (BN = 64) or 32 (BN = 128)
+      static_assert(kRowLanes * 4 == BN, "four columns per lane");
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = si.row0 + 4 * g + r;
-        uint64_t k1 = 0, k2 = 0;
-        if (row < si.row_end && col0 < N) k1 = rr::dev::gate_key(acc[0][r], col0);
-        rr::dev::merge_top2_row16(k1, k2);
-        if (li == 0) {
-          s_keys[(wave * kRows + 4 * g + r) * 2] = k1;
-          s_keys[(wave * kRows + 4 * g + r) * 2 + 1] = k2;
-        }
-      }
+      for (int r = 0; r < 4; ++r) s_lg[(4 * g + r) * kLgLd + col0] = acc[0][r];
       __syncthreads();
       const int rows = si.row_end - si.row0 < kRows ? si.row_end - si.row0 : kRows;
-      if (tid < rows) {
-        uint64_t k1 = 0, k2 = 0;
+      const int my_row = tid / kRowLanes;
+      const int c0 = 4 * (tid % kRowLanes);
+      const v4f lg = *reinterpret_cast<const v4f*>(s_lg + my_row * kLgLd + c0);
+      uint64_t k1 = 0, k2 = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          rr::dev::insert_key(s_keys[(w * kRows + tid) * 2], k1, k2);
-          rr::dev::insert_key(s_keys[(w * kRows + tid) * 2 + 1], k1, k2);
-        }
+      for (int j = 0; j < 4; ++j) {
+        if (c0 + j < N) rr::dev::insert_key(rr::dev::gate_key(lg[j], c0 + j), k1, k2);
+      }
+      rr::dev::merge_top2_row16(k1, k2);
+      if constexpr (kRowLanes == 32) {  // the row's other 16 lanes
+        rr::dev::merge_pair(k1, k2, rr::dev::shfl_xor_u64(k1, 16), rr::dev::shfl_xor_u64(k2, 16));
+      }
+      if (tid % kRowLanes == 0 && my_row < rows) {
         float w1, w2;
         rr::dev::gate_weights(k1, k2, &w1, &w2);
-        const std::size_t row = static_cast<std::size_t>(si.row0 + tid);
+        const std::size_t row = static_cast<std::size_t>(si.row0 + my_row);
         p.gate_ids[2 * row] = rr::dev::key_expert(k1);
         p.gate_ids[2 * row + 1] = rr::dev::key_expert(k2);
         p.gate_weights[2 * row] = w1;
@@ -881,7 +881,7 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   const std::size_t stage = static_cast<std::size_t>(bn + kRows) * (chunks * 16 + 4);
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
-  if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(waves) * kRows * 2 * sizeof(uint64_t);
+  if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
   bytes += kMaxBlocks * 64 * sizeof(int32_t);
   if (mode == kStripChain) {
     bytes += static_cast<std::size_t>(waves) * kMaxSegs * 8 * sizeof(int32_t);  // segment lists
