@@ -90,8 +90,9 @@ struct TileShape {
 
 // Global -> register staging of one BK slice. A rows are k-contiguous in
 // global memory; B rows are n-contiguous and are transposed on the LDS store.
-// src_rows (LDS, optional) maps tile row r to its source row of A (-1: none);
-// without it tile row r is row row0 + r, valid below row_end. (Loading from
+// set_rows resolves, once per tile, the A row behind each of the thread's A
+// slots: src_rows (LDS, optional) maps tile row r to its source row of A (-1:
+// none); without it tile row r is row row0 + r, valid below row_end. (Loading from
 // clamped addresses and zeroing at the LDS store, as the strip kernel does,
 // measured slower here: C4 grouped GEMM 17.1 ms against 15.6 ms, the selects
 // adding VALU work to every k step of an MFMA-bound loop.)
@@ -104,31 +105,52 @@ template <class S, bool VEC>
 struct Stage {
   float a[S::kALoads][4];
   float b[S::kBLoads][4];
+  // A slot p: its row's element at the slot's column; slots without a row
+  // point at row 0 (a valid address, never read: row_ok is false).
+  const float* arow[S::kALoads];
+  bool row_ok[S::kALoads];
+  float* xrow[S::kALoads];  // chain: the same element of the x_permuted row (nullptr: none)
 
-  __device__ __forceinline__ void load(const float* __restrict__ A, const float* __restrict__ B,
-                                       const int32_t* src_rows, int row0, int row_end, int n0,
-                                       int N, int K, int k0, int tid) {
+  // Once per tile: the thread's A slots (and x_permuted rows, when given).
+  __device__ __forceinline__ void set_rows(const float* __restrict__ A, const int32_t* src_rows,
+                                           int row0, int row_end, int K, float* x_permuted,
+                                           int tid) {
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
       const int r = f / (S::BK / 4);  // BK / 4 float4 per row
       const int c = (f % (S::BK / 4)) * 4;
       const int src = src_rows != nullptr ? src_rows[r] : (row0 + r < row_end ? row0 + r : -1);
+      row_ok[p] = src >= 0;
+      arow[p] = A + static_cast<std::size_t>(src >= 0 ? src : 0) * K + c;
+      xrow[p] = src >= 0 && x_permuted != nullptr
+                    ? x_permuted + static_cast<std::size_t>(row0 + r) * K + c
+                    : nullptr;
+    }
+  }
+
+  __device__ __forceinline__ void load(const float* __restrict__ B, int n0, int N, int K, int k0,
+                                       int tid) {
+#pragma unroll
+    for (int p = 0; p < S::kALoads; ++p) {
+      const int f = tid + p * S::kThreads;
+      const int c = (f % (S::BK / 4)) * 4;
       const int k = k0 + c;
-      const float* ptr = A + static_cast<std::size_t>(src < 0 ? 0 : src) * K + k;
+      const bool has_row = row_ok[p];
+      const float* ptr = arow[p] + k0;
       if (VEC) {
-        if (src >= 0 && k < K) {
+        if (has_row && k < K) {
           const float4 v = *reinterpret_cast<const float4*>(ptr);
           a[p][0] = v.x; a[p][1] = v.y; a[p][2] = v.z; a[p][3] = v.w;
         } else {
           a[p][0] = a[p][1] = a[p][2] = a[p][3] = 0.0F;
         }
-      } else if (src >= 0 && k + 3 < K) {  // whole quad: one 16-byte load (4-byte aligned)
+      } else if (has_row && k + 3 < K) {  // whole quad: one 16-byte load (4-byte aligned)
         const f4u v = *reinterpret_cast<const f4u*>(ptr);
         a[p][0] = v.x; a[p][1] = v.y; a[p][2] = v.z; a[p][3] = v.w;
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[p][j] = (src >= 0 && k + j < K) ? ptr[j] : 0.0F;
+        for (int j = 0; j < 4; ++j) a[p][j] = (has_row && k + j < K) ? ptr[j] : 0.0F;
       }
     }
 #pragma unroll
@@ -177,18 +199,16 @@ struct Stage {
     }
   }
 
-  // Writes the staged A slice to rows [row0, row0 + BM) of out (the gathered
-  // x_permuted rows of the chain), valid rows and columns only.
-  __device__ __forceinline__ void store_a_rows(float* __restrict__ out, const int32_t* src_rows,
-                                               int row0, int K, int k0, int tid) const {
+  // Writes the staged A slice to the x_permuted rows of the tile (the gathered
+  // rows of the chain), valid rows and columns only.
+  __device__ __forceinline__ void store_a_rows(int K, int k0, int tid) const {
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
-      const int r = f / (S::BK / 4);
       const int c = (f % (S::BK / 4)) * 4;
       const int k = k0 + c;
-      if (src_rows[r] < 0) continue;
-      float* ptr = out + static_cast<std::size_t>(row0 + r) * K + k;
+      if (xrow[p] == nullptr) continue;
+      float* ptr = xrow[p] + k0;
       if (VEC) {
         if (k < K) *reinterpret_cast<float4*>(ptr) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
       } else if (k + 3 < K) {
@@ -318,16 +338,17 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
       for (int j = 0; j < S::kTN; ++j) acc[i][j] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
 
     Stage<S, VEC> st;
+    st.set_rows(prm.X, src_rows, row0, row_end, K, write_xp ? prm.x_permuted : nullptr, tid);
     if (nk > 0) {
-      st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, 0, tid);
+      st.load(B, n0, N, K, 0, tid);
       st.store(stages, tid);
-      if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, 0, tid);
+      if (write_xp) st.store_a_rows(K, 0, tid);
     }
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
       if (S::kStages > 1 && kt + 1 < nk) {
-        st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+        st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
       }
       const float* As = cur;
       const float* Bs = cur + S::BM * S::kLd;
@@ -355,12 +376,12 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
       }
       if (S::kStages > 1 && kt + 1 < nk) {
         st.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
-        if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, (kt + 1) * S::BK, tid);
+        if (write_xp) st.store_a_rows(K, (kt + 1) * S::BK, tid);
       } else if (S::kStages == 1 && kt + 1 < nk) {
         __syncthreads();  // every wave is done with the single stage
-        st.load(prm.X, B, src_rows, row0, row_end, n0, N, K, (kt + 1) * S::BK, tid);
+        st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
         st.store(stages, tid);
-        if (write_xp) st.store_a_rows(prm.x_permuted, src_rows, row0, K, (kt + 1) * S::BK, tid);
+        if (write_xp) st.store_a_rows(K, (kt + 1) * S::BK, tid);
       }
       __syncthreads();
     }
