@@ -303,10 +303,14 @@ hipError_t histogram_atomic(const int32_t* ids, int32_t* counts, int32_t* offset
   rr_hist_zero_kernel<<<(experts + 255) / 256, 256, 0, stream>>>(counts, experts);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  // one pass of kHistPass ids per block up to 512 blocks; larger R (or many
-  // experts, whose per-block global adds grow with E) take several passes
+  // one pass of kHistPass ids per block up to 128 blocks; larger R (or many
+  // experts, whose per-block global adds grow with E) take several passes.
+  // Every block adds its nonzero bins into the global counts, so each count
+  // takes one atomic per block, serialised at the memory side: at R = 2^20,
+  // 128 blocks measured 8.8 / 9.2 us (E = 33 / 256) against 9.4 / 11.1 with
+  // 256 and 11.1 / 11.6 with 32 (fewer blocks crowd the hot-expert bins).
   const long passes = (static_cast<long>(routes) + kHistPass - 1) / kHistPass;
-  long blocks = passes < 512 ? passes : 512;
+  long blocks = passes < 128 ? passes : 128;
   const long by_experts = static_cast<long>(routes) / (8L * experts);  // >= 8 ids per global add
   if (blocks > by_experts) blocks = by_experts > 0 ? by_experts : 1;
   const long per_block = (passes + blocks - 1) / blocks;
