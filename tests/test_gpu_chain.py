@@ -290,3 +290,35 @@ def test_fused_launches_one_by_one_equal_chain(ctx, device, kind, hidden):
         b = whole[key]
         assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
                               b.view(np.uint32) if b.dtype == np.float32 else b), f"{key} differs"
+
+
+@pytest.mark.parametrize("experts", [64, 128])
+def test_fused_router_gate_special_values(ctx, device, experts):
+    """Token rows that make NaN, +-Inf and all-equal logits go through the
+    router's fused gate epilogue (16 or 32 lanes per row): ids and weights
+    match the dense GEMM + top-2 gate operators bit for bit and the oracle
+    top-2 of the device logits (NaN ranks as -Inf; equal values -> {0.5, 0.5};
+    +Inf first -> {1, 0})."""
+    cfg = workloads.ChainConfig("special", 96, experts, 64, 32, from_tokens=True)
+    inp = workloads.chain_inputs(cfg, seed=5)
+    x = inp["x"].copy()
+    x[0, :] = np.nan               # every logit NaN -> ids {0, 1}, weights {0.5, 0.5}
+    x[1, :] = 0.0                  # every logit 0 -> ids {0, 1}, weights {0.5, 0.5}
+    x[2, :] = 0.0
+    x[2, 5] = np.inf               # +-Inf or NaN logits, by the sign of router row 5
+    x[3, 7] = -np.inf
+    x[4, :] = 1e30                 # logits overflow to +-Inf
+    inp["x"] = x
+    run = ChainRun(cfg, inp, device)
+    fused = run.run(ctx)
+    ref = run_stages(cfg, inp, device, ctx)
+    for key in ("logits", "ids", "weights"):
+        a, b = fused[key], ref[key]
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), key
+    ids, w = oracle.top2_f32(fused["logits"])
+    assert np.array_equal(fused["ids"], ids)
+    fails, max_abs, _ = oracle.compare_floating(fused["weights"], w, 1e-6, 1e-6)  # device vs host expf
+    assert fails == 0, max_abs
+    assert fused["ids"][0].tolist() == [0, 1] and fused["weights"][0].tolist() == [0.5, 0.5]
+    assert fused["ids"][1].tolist() == [0, 1] and fused["weights"][1].tolist() == [0.5, 0.5]
