@@ -302,8 +302,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   constexpr int kLgLd = BN + 4;       // router: padded row of the logit tile
   float* s_lg = As + kRows * kLd;      // router: [16][kLgLd] logits of the strip
   int32_t* s_cnt = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
-  int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][8] (16-byte aligned)
-  int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 8 : 0);  // chain: [max_strips * 16]
+  int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][4] (16-byte aligned)
+  int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 4 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
   // chain: [max_strips * 16] token of each slot's route (-1: none), [max_strips][4] strip info
   int32_t* s_tok = reinterpret_cast<int32_t*>(s_w + (MODE == kStripChain ? p.max_strips * kRows : 0));
@@ -516,7 +516,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     // and readlanes, uniform control flow only) runs once per wave into the
     // wave's own LDS rows; the passes read them back (LDS operations of one
     // wave complete in order, so no barrier is needed).
-    int32_t* s_segs = s_seglist + wave * kMaxSegs * 8;  // [kMaxSegs][e, lo, hi, base, off]
+    int32_t* s_segs = s_seglist + wave * kMaxSegs * 4;  // [kMaxSegs][e, lo, hi, base]
     int nseg = 0;
     {
 #pragma unroll 1
@@ -527,24 +527,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         const int end_e = pre_e + strips_of(rows_e);
         const int last = s1 < end_e ? s1 : end_e;
         const int hi = (last - pre_e) * kRows;
-        const int off_e = seg_field(tab.off, e);
         if (lane == 0) {
-          int32_t* d = s_segs + nseg * 8;
-          *reinterpret_cast<int4*>(d) =
+          *reinterpret_cast<int4*>(s_segs + nseg * 4) =
               make_int4(e, (s - pre_e) * kRows, hi < rows_e ? hi : rows_e, (pre_e - s0) * kRows);
-          d[4] = off_e;
         }
         s = last > s ? last : s1;  // always advances
       }
     }
     struct Seg {
-      int e, lo, hi, base, off;
+      int e, lo, hi, base;
     };
     auto seg_read = [&](int i) -> Seg {
-      const int4 v = *reinterpret_cast<const int4*>(s_segs + i * 8);
+      const int4 v = *reinterpret_cast<const int4*>(s_segs + i * 4);
       return Seg{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
-                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w),
-                 __builtin_amdgcn_readfirstlane(s_segs[i * 8 + 4])};
+                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
     };
     auto matches = [](const int4& v, int e) -> int32_t {
       return (v.x == e ? 1 : 0) + (v.y == e ? 1 : 0) + (v.z == e ? 1 : 0) + (v.w == e ? 1 : 0);
@@ -587,13 +583,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     if (s0 < s1) load_b(cur.e);
     // route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows
-    int row = 0;
-#pragma unroll 1
-    for (int i = 0; i < nseg; ++i) {
-      const Seg sg = seg_read(i);
-      if (tid >= sg.base + sg.lo && tid < sg.base + sg.hi) row = sg.off + (tid - sg.base);
-    }
     if (tid < slots) {  // slots <= (kMaxSegs + 1) * 16 <= kThreads
+      // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
+      const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
       const int32_t route = s_slot[tid];
       s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
       if (route >= 0) {
@@ -884,7 +876,7 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
   bytes += kMaxBlocks * 64 * sizeof(int32_t);
   if (mode == kStripChain) {
-    bytes += static_cast<std::size_t>(waves) * kMaxSegs * 8 * sizeof(int32_t);  // segment lists
+    bytes += static_cast<std::size_t>(waves) * kMaxSegs * 4 * sizeof(int32_t);  // segment lists
     bytes += 3 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);  // slots, weights, tokens
     bytes += static_cast<std::size_t>(max_strips) * 4 * sizeof(int32_t);          // strip info
     bytes += static_cast<std::size_t>(waves) * 64 * ((segments + 63) / 64) * sizeof(int32_t);  // per-wave histograms
