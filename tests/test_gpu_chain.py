@@ -322,3 +322,28 @@ def test_fused_router_gate_special_values(ctx, device, experts):
     assert fails == 0, max_abs
     assert fused["ids"][0].tolist() == [0, 1] and fused["weights"][0].tolist() == [0.5, 0.5]
     assert fused["ids"][1].tolist() == [0, 1] and fused["weights"][1].tolist() == [0.5, 0.5]
+
+
+@pytest.mark.parametrize("experts", list(range(4, 129, 4)))
+def test_router_gate_sweep(ctx, device, experts):
+    """The chain's router launch (GEMM + fused top-2) for every E the strip
+    router takes (E % 4 == 0, E <= 128; 16 lanes per row up to E = 64, 32
+    above) at T = 65 (a ragged last strip) with exact ties in the router
+    weights: ids are the oracle top-2 of the device logits, weights within the
+    reference's 1e-6."""
+    cfg = workloads.ChainConfig("router", 65, experts, 32, 8, from_tokens=True)
+    inp = workloads.chain_inputs(cfg, seed=experts)
+    wr = inp["router_weights"].copy()
+    wr[:, experts // 2] = wr[:, 0]  # identical columns -> exactly tied logits
+    inp["router_weights"] = wr
+    run = ChainRun(cfg, inp, device)
+    c = rr.RuntimeContext(stream=ctx.stream, workspace=run.ws.data_ptr(),
+                          workspace_bytes=run.ws.numel() * 4, architecture=ctx.architecture)
+    assert rr.chain_fused_launch_names(run.args, True)[0] == "router_gate"
+    status = rr.chain_fused_launch(run.args, c, True, 0)
+    assert status.ok(), status.message
+    logits, ids, w = to_host(run.logits), to_host(run.ids), to_host(run.w)
+    e_ids, e_w = oracle.top2_f32(logits)
+    assert np.array_equal(ids, e_ids)
+    fails, max_abs, _ = oracle.compare_floating(w, e_w, 1e-6, 1e-6)
+    assert fails == 0, max_abs
