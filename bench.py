@@ -660,6 +660,14 @@ def main() -> int:
             extras["C1"] = small_chain(torch, device, workloads.C1)
         if "c2" in only:
             extras["C2"] = small_chain(torch, device, workloads.C2)
+        if "c1" in only:
+            # the only shape with a published reference chain time (not a
+            # BASELINE config; other hardware): context, not vs_baseline
+            ref = small_chain(torch, device, workloads.ChainConfig("reference_l3", 512, 64, 128, 128))
+            ref["reference_published"] = {
+                "p50_us": 69.734, "hardware": "RTX 3080 (SM86)",
+                "source": "reference docs/reports/l3_three_way_20260805/RaggedRoute_L3_3way_comparison.md:7,51"}
+            extras["reference_l3_shape"] = ref
         if "c4" in only:
             extras["C4"] = c4(torch, device, cpu_sample=not args.quick)
         if "c4u" in only:
