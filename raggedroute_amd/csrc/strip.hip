@@ -168,6 +168,9 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
 
 struct StripRange {
   int s0, s1;
+  // Segment-aligned ranges: all strips lie in segment e, whose strips start
+  // at pre, rows at off, cnt rows (e = -1: the range may span segments).
+  int e, pre, off, cnt;
 };
 
 // ceil(x / m) in 32-bit unsigned arithmetic (x >= 0, m >= 1).
@@ -184,6 +187,8 @@ __device__ __forceinline__ StripRange even_range(int total, int grid, int worker
   StripRange r;
   r.s0 = worker * q + (worker < rem ? worker : rem);
   r.s1 = r.s0 + q + (worker < rem ? 1 : 0);
+  r.e = -1;
+  r.pre = r.off = r.cnt = 0;
   return r;
 }
 
@@ -226,6 +231,8 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
   }
   StripRange r;
   r.s0 = r.s1 = 0;
+  r.e = -1;
+  r.pre = r.off = r.cnt = 0;
   if (worker < carry) {
     int e = 0;
 #pragma unroll
@@ -238,10 +245,15 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
     }
     const int first = seg_field(wpre, e);
     const int pre_e = seg_field(t.pre, e);
-    const int end_e = pre_e + strips_of(seg_field(t.cnt, e));
+    const int cnt_e = seg_field(t.cnt, e);
+    const int end_e = pre_e + strips_of(cnt_e);
     r.s0 = pre_e + (worker - first) * m;
     r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
     if (r.s0 > r.s1) r.s0 = r.s1;
+    r.e = e;
+    r.pre = pre_e;
+    r.off = seg_field(t.off, e);
+    r.cnt = cnt_e;
   }
   return r;
 }
@@ -464,21 +476,23 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   }
 
   const int total = tab.total_strips;
-  int s0, s1;
+  StripRange range;
   if constexpr (kSingle) {
-    const StripRange range = even_range(total, grid, worker);
-    s0 = range.s0;
-    s1 = range.s1;
+    range = even_range(total, grid, worker);
   } else {
-    const StripRange range = assign_strips(tab, nblk, E, total, grid, worker,
-                                           MODE == kStripChain ? p.max_strips : INT_MAX);
-    s0 = range.s0;
-    s1 = range.s1;
+    range = assign_strips(tab, nblk, E, total, grid, worker,
+                          MODE == kStripChain ? p.max_strips : INT_MAX);
   }
+  const int s0 = range.s0;
+  const int s1 = range.s1;
   auto info = [&](int s) -> StripInfo {
     if constexpr (kSingle) {
       return StripInfo{0, s * kRows, p.M, s * kRows};
     } else {
+      if (range.e >= 0) {  // segment-aligned range: arithmetic, no lookup
+        const int rank0 = (s - range.pre) * kRows;
+        return StripInfo{range.e, range.off + rank0, range.off + range.cnt, rank0};
+      }
       return strip_info(tab, nblk, E, s);
     }
   };
@@ -493,7 +507,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     // after the barrier that ends the rank passes).
 #pragma unroll 1
     for (int k = wave; k < s1 - s0; k += kWaves) {
-      const StripInfo si = strip_info(tab, nblk, E, s0 + k);
+      const StripInfo si = info(s0 + k);
       if (lane == 0) *reinterpret_cast<int4*>(s_info + 4 * k) = make_int4(si.e, si.row0, si.row_end, si.rank0);
     }
   }
@@ -518,7 +532,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     // wave complete in order, so no barrier is needed).
     int32_t* s_segs = s_seglist + wave * kMaxSegs * 4;  // [kMaxSegs][e, lo, hi, base]
     int nseg = 0;
-    {
+    if (range.e >= 0) {
+      // segment-aligned range: one segment, no walk
+      if (s0 < s1) {
+        const int hi = (s1 - range.pre) * kRows;
+        if (lane == 0) {
+          *reinterpret_cast<int4*>(s_segs) = make_int4(range.e, (s0 - range.pre) * kRows,
+                                                       hi < range.cnt ? hi : range.cnt,
+                                                       (range.pre - s0) * kRows);
+        }
+        nseg = 1;
+      }
+    } else {
 #pragma unroll 1
       for (int s = s0; s < s1 && nseg < kMaxSegs; ++nseg) {
         const int e = seg_find(tab, nblk, E, s);
