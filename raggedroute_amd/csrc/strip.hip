@@ -202,17 +202,16 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
   const int lane = lane_id();
   const int m0 = total > 0 ? (total + grid - 1) / grid : 1;
   const int m1 = m0 + 1;
-  int32_t need0 = 0, need1 = 0;
+  auto need = [&](int m) {
+    int32_t n = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxBlocks; ++j) {
-    if (j < nblk) {
-      const int32_t st = strips_of(t.cnt[j]);
-      need0 += wave_sum(ceil_div32(st, m0));
-      need1 += wave_sum(ceil_div32(st, m1));
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      if (j < nblk) n += wave_sum(ceil_div32(strips_of(t.cnt[j]), m));
     }
-  }
-  const bool fit0 = need0 <= grid && m0 <= cap;
-  const bool fit1 = need1 <= grid && m1 <= cap;
+    return n;
+  };
+  const bool fit0 = m0 <= cap && need(m0) <= grid;
+  const bool fit1 = !fit0 && m1 <= cap && need(m1) <= grid;  // (only asked when m0 fails)
   if (!fit0 && !fit1) return even_range(total, grid, worker);
   const int m = fit0 ? m0 : m1;
   // workers of segment e: [wpre_e, wpre_e + ceil(strips_e / m))
@@ -313,8 +312,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   float* As = Bs + BN * kLd;      // [16][kLd]: A rows of the current strip
   constexpr int kLgLd = BN + 4;       // router: padded row of the logit tile
   float* s_lg = As + kRows * kLd;      // router: [16][kLgLd] logits of the strip
-  int32_t* s_cnt = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
-  int32_t* s_seglist = s_cnt + kMaxBlocks * 64;  // chain: [waves][kMaxSegs][4] (16-byte aligned)
+  // chain: [waves][kMaxSegs][4] segment lists (16-byte aligned)
+  int32_t* s_seglist = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 4 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
   // chain: [max_strips * 16] token of each slot's route (-1: none), [max_strips][4] strip info
@@ -382,11 +381,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     const int nchunks = (R + 255) >> 8;
     c_begin = wave * nchunks / kWaves;
     c_end = (wave + 1) * nchunks / kWaves;
-    for (int i = tid; i < kWaves * 64 * nblk; i += kThreads) s_cntw[i] = 0;
-    // Empty route slots of every strip this workgroup may own: cleared here,
-    // barriers before the rank passes, whose waves fill slots that another
-    // wave's thread would otherwise clear (a clear racing a fill loses the route).
-    for (int i = tid; i < p.max_strips * kRows; i += kThreads) s_slot[i] = -1;
     // Every chunk load is issued before any is used (a select or a branch
     // between them would wait for each in turn): clamped in-bounds addresses,
     // validity applied afterwards, the ragged tail (R % 4 != 0) read last.
@@ -398,6 +392,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         idv[u] = *reinterpret_cast<const int4*>(p.ids + (r + 3 < R ? r : R - 4));
       }
     }
+    // (LDS clears while the id loads are in flight)
+    for (int i = tid; i < kWaves * 64 * nblk; i += kThreads) s_cntw[i] = 0;
+    // Empty route slots of every strip this workgroup may own: cleared here,
+    // barriers before the rank passes, whose waves fill slots that another
+    // wave's thread would otherwise clear (a clear racing a fill loses the route).
+    for (int i = tid; i < p.max_strips * kRows; i += kThreads) s_slot[i] = -1;
 #pragma unroll
     for (int u = 0; u < kIdChunks; ++u) {
       const int r = (c_begin + u) * 256 + 4 * lane;
@@ -427,15 +427,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       }
     }
     __syncthreads();
-    for (int e = tid; e < 64 * nblk; e += kThreads) {
+    // every wave sums the waves' rows itself (no combined row, no second barrier)
+#pragma unroll
+    for (int j = 0; j < kMaxBlocks; ++j) {
       int32_t total = 0;
+      if (j < nblk) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) total += s_cntw[w * 64 * nblk + e];
-      s_cnt[e] = total;
+        for (int w = 0; w < kWaves; ++w) total += s_cntw[w * 64 * nblk + 64 * j + lane];
+      }
+      tab.cnt[j] = total;
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kMaxBlocks; ++j) tab.cnt[j] = j < nblk ? s_cnt[64 * j + lane] : 0;
   } else if constexpr (MODE == kStripGrouped) {
 #pragma unroll
     for (int j = 0; j < kMaxBlocks; ++j) {
@@ -899,7 +900,6 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
-  bytes += kMaxBlocks * 64 * sizeof(int32_t);
   if (mode == kStripChain) {
     bytes += static_cast<std::size_t>(waves) * kMaxSegs * 4 * sizeof(int32_t);  // segment lists
     bytes += 3 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);  // slots, weights, tokens
