@@ -568,14 +568,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       return Seg{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                  __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
     };
-    auto matches = [](const int4& v, int e) -> int32_t {
-      return (v.x == e ? 1 : 0) + (v.y == e ? 1 : 0) + (v.z == e ? 1 : 0) + (v.w == e ? 1 : 0);
-    };
     // Stable ranks (route order = wave, chunk, lane, component): a segment's
     // routes in the chunks of the waves before mine are the sum of those
-    // waves' histogram rows; inside a chunk, the exclusive scan of the
-    // per-lane match counts over the wave gives each lane's first rank. Keep
-    // the ranks that fall in my strips.
+    // waves' histogram rows; inside a chunk, one ballot per component gives
+    // the matches of every lane, so a lane's first rank is the count of
+    // matches in the lanes before it (mbcnt over the four masks) and the
+    // chunk's total is their popcount. Keep the ranks that fall in my strips.
 #pragma unroll 1
     for (int i = 0; i < nseg; ++i) {
       const Seg sg = seg_read(i);
@@ -586,11 +584,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
 #pragma unroll
       for (int u = 0; u < kIdChunks; ++u) {
         if (c_begin + u < c_end && q < sg.hi) {
-          const int32_t m = matches(idv[u], sg.e);
-          const int32_t incl = rr::dev::wave_inclusive_scan(m);
-          int rank = q + incl - m;
-          const int r = (c_begin + u) * 256 + 4 * lane;
           const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+          uint32_t before = 0;  // matches in the lanes below mine
+          int32_t chunk = 0;    // matches in the chunk
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint64_t mk = __ballot(vals[k] == sg.e);
+            before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mk >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), before));
+            chunk += __builtin_popcountll(mk);
+          }
+          int rank = q + static_cast<int>(before);
+          const int r = (c_begin + u) * 256 + 4 * lane;
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             if (vals[k] == sg.e) {
@@ -598,7 +603,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
               ++rank;
             }
           }
-          q += __builtin_amdgcn_readlane(incl, 63);
+          q += chunk;
         }
       }
     }
