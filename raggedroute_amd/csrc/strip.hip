@@ -5,12 +5,13 @@
 // Work unit: a strip = 16 rows of one segment (expert) x every output column.
 // One persistent workgroup per CU owns a contiguous range of strips; wave w
 // computes columns [16 w, 16 w + 16) of each strip (BN / 16 waves).
-//   B (the segment's [K, N] weights) is resident in LDS for as long as the
-//     workgroup stays on that segment: it is fetched with coalesced loads
-//     (each lane quad reads 64 contiguous bytes of a k row, a wave 16 rows)
-//     and transposed into
-//     [n][K + 4] rows, whose padding keeps both the transposing stores and the
-//     ds_read_b128 operand fetches free of bank conflicts.
+//   B (the segment's [K, N] weights) stays in registers for as long as the
+//     workgroup stays on that segment: wave w holds its own 16 columns for the
+//     whole K in MFMA operand order (lane (li, g) holds B[16c + 4g + s][16w + li],
+//     64 floats), loaded straight from global memory (one load instruction
+//     reads 64 contiguous bytes of four k rows). B needs no LDS stage, no
+//     transposing stores and no barrier, and the first strip's MFMAs wait for
+//     each k chunk of B as it arrives rather than for all of it.
 //   A rows (16 x K) are loaded by the whole workgroup with row-contiguous
 //     float4 accesses into registers, stored to a [16][K + 4] LDS stage, and
 //     the next strip's rows are loaded while the current strip's MFMAs run.
@@ -290,11 +291,9 @@ template <int BN, int WAVES, int MODE, int CHUNKS>
 __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParams p) {
   constexpr int kWaves = WAVES;
   constexpr int kTiles = BN / 16 / WAVES;              // 16-column MFMA tiles per wave
-  static_assert(kTiles * 16 * WAVES == BN && (kTiles == 1 || kTiles == 2), "waves x tiles = BN / 16");
+  static_assert(kTiles * 16 * WAVES == BN && kTiles == 1, "one 16-column tile per wave (B in its registers)");
   static_assert(MODE != kStripRouterGate || kTiles == 1, "the gate merge takes one tile per wave");
   constexpr int kThreads = kWaves * 64;
-  constexpr int kNB = BN / 16;                         // 16-column blocks of B
-  constexpr int kBLoads = kMaxChunks * kNB / kWaves;   // float4 B loads per lane (whole K)
   constexpr int kIdChunks = kMaxRoutes / 256 / kWaves; // route-id chunks per wave
   constexpr int kRowThreads = kThreads / kRows;        // A staging: threads per row
   constexpr int kALoads = 64 / kRowThreads;            // float4 per thread (K <= 256)
@@ -308,8 +307,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   const int nblk = (E + 63) >> 6;
   const int chunks = CHUNKS > 0 ? CHUNKS : (K + 15) >> 4;
   const int kLd = chunks * 16 + 4;
-  float* Bs = lds;                // [BN][kLd]: B of the current segment, k contiguous
-  float* As = Bs + BN * kLd;      // [16][kLd]: A rows of the current strip
+  float* As = lds;                // [16][kLd]: A rows of the current strip
   constexpr int kLgLd = BN + 4;       // router: padded row of the logit tile
   float* s_lg = As + kRows * kLd;      // router: [16][kLgLd] logits of the strip
   // chain: [waves][kMaxSegs][4] segment lists (16-byte aligned)
@@ -333,41 +331,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // weights through the same L2.
   const int worker = (grid % kXcds == 0) ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
 
-  // ---- B of a segment: whole K in registers, then transposed into LDS ----
-  // Four consecutive lanes read one contiguous 64-byte row segment (the
-  // memory pipeline merges a quad's accesses); a wave load covers 16 k rows.
-  v4f breg[kBLoads];
-  const int bks = lane >> 2;
-  const int bnq = lane & 3;
+  // ---- B of a segment: this wave's 16 columns, whole K, in registers ----
+  // bq[c][s] = B[16c + 4g + s][16 wave + li]: sixteen lanes read 64
+  // contiguous bytes of one k row, a load instruction four rows. Columns past
+  // N read column N - 1 (their outputs are never stored); rows past K read row
+  // K - 1 and are zeroed where they are used.
+  float bq[kMaxChunks][4];
   auto load_b = [&](int e) {
     const float* W = p.W + static_cast<std::size_t>(e) * K * N;
+    const int n = 16 * wave + li;
+    const int nc = n < N ? n : N - 1;
 #pragma unroll
-    for (int u = 0; u < kBLoads; ++u) {
-      const int blk = wave + kWaves * u;
-      const int k = (blk / kNB) * 16 + bks;
-      const int n = (blk % kNB) * 16 + 4 * bnq;
-      const int kc = k < K ? k : K - 1;
-      const int nc = n < N ? n : N - 4;
-      breg[u] = load_raw(W + static_cast<std::size_t>(kc) * N + nc);
-    }
-  };
-  auto store_b = [&]() {
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c < chunks) {
 #pragma unroll
-    for (int u = 0; u < kBLoads; ++u) {
-      const int blk = wave + kWaves * u;
-      if (blk < chunks * kNB) {
-        const int k = (blk / kNB) * 16 + bks;
-        const int n = (blk % kNB) * 16 + 4 * bnq;
-        float* dst = Bs + n * kLd + k;
-        const v4f v = zero_unless(k < K && n < N, breg[u]);
-        dst[0] = v.x;
-        dst[kLd] = v.y;
-        dst[2 * kLd] = v.z;
-        dst[3 * kLd] = v.w;
+        for (int s = 0; s < 4; ++s) {
+          const int k = 16 * c + 4 * g + s;
+          bq[c][s] = W[(k < K ? k : K - 1) * N + nc];  // (K * N < 2^31: K <= 256, N <= 128)
+        }
       }
     }
   };
-  if constexpr (MODE == kStripDense || MODE == kStripRouterGate) load_b(0);
 
   // ---------------------------------------------------------------- segments
   SegTable tab;
@@ -498,10 +482,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     }
   };
   StripInfo cur{};
-  if (s0 < s1) {
-    cur = info(s0);
-    if constexpr (MODE == kStripGrouped) load_b(cur.e);  // in flight below
-  }
+  if (s0 < s1) cur = info(s0);
   if constexpr (MODE == kStripChain) {
     // Every strip's info, once and in parallel (wave w: strips s0 + w,
     // s0 + w + waves, ...), for the strip loop to read back from LDS (read
@@ -525,7 +506,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // ------------------------------------------- chain: routes of my strips
   float w_pending = 0.0F;
   if constexpr (MODE == kStripChain) {
-    const int slots = (s1 - s0) * kRows;
     // My segments: segment e covers my strips [s, last), i.e. its stable
     // ranks [lo, hi), stored from slot base + rank. The walk (ballot lookups
     // and readlanes, uniform control flow only) runs once per wave into the
@@ -608,23 +588,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       }
     }
     __syncthreads();
-    // B of the first segment: issued after the rank passes, whose waves would
-    // otherwise stall behind the 16 loads each, and in flight with the route
-    // map below.
-    if (s0 < s1) load_b(cur.e);
-    // route map entries of my rows; the route weights are loaded now and
-    // stored to LDS with the first strip's A rows
-    if (tid < slots) {  // slots <= (kMaxSegs + 1) * 16 <= kThreads
-      // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
-      const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
-      const int32_t route = s_slot[tid];
-      s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
-      if (route >= 0) {
-        p.route_pos[route] = row;
-        if (p.sorted_route != nullptr) p.sorted_route[row] = route;
-        if (p.combine) w_pending = p.route_weights[route];
-      }
-    }
   }
 
   // ------------------------------------------------------------ strip loop
@@ -707,19 +670,34 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   StripInfo prev{};
   bool pending = false;
 
-  int cur_e = -1;
+  // Issue order: the first strip's A rows, the route map's weight loads,
+  // then B. Memory operations complete in order, so the A stage waits for
+  // A and the weights alone, and the first strip's MFMAs wait for B one k
+  // chunk at a time.
   int src = -1;
   if (s0 < s1) {
     src = a_source(s0, cur);
     load_a(src);
   }
+  if constexpr (MODE == kStripChain) {
+    // Route map entries of my rows; the route weights are loaded now and
+    // stored to LDS with the first strip's A rows.
+    if (tid < (s1 - s0) * kRows) {  // <= (kMaxSegs + 1) * 16 <= kThreads
+      // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
+      const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
+      const int32_t route = s_slot[tid];
+      s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
+      if (route >= 0) {
+        p.route_pos[route] = row;
+        if (p.sorted_route != nullptr) p.sorted_route[row] = route;
+        if (p.combine) w_pending = p.route_weights[route];
+      }
+    }
+  }
+  if (s0 < s1) load_b(cur.e);
   for (int s = s0; s < s1; ++s) {
     const StripInfo si = cur;
-    __syncthreads();  // every wave is done with As (and with Bs, if it changes)
-    if (si.e != cur_e) {
-      store_b();  // breg holds B of si.e (loaded ahead)
-      cur_e = si.e;
-    }
+    __syncthreads();  // every wave is done with As
     // ---- this strip's A rows -> LDS (zeros past K up to the chunk edge) ----
 #pragma unroll
     for (int u = 0; u < kALoads; ++u) {
@@ -740,12 +718,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       if (s == s0 && tid < (s1 - s0) * kRows) s_w[tid] = w_pending;
     }
     __syncthreads();
-    // ---- prefetch the next strip's A rows (and B of its segment) ----
+    // ---- prefetch the next strip's A rows (B of a new segment follows the
+    // MFMAs, which still read this segment's B) ----
     if (s + 1 < s1) {
       cur = next_info(s + 1);
       src = a_source(s + 1, cur);
       load_a(src);
-      if (cur.e != si.e) load_b(cur.e);
     }
 
     // ---- MFMA: acc[t] = rows x columns [col0 + 16 t - li, + 16) ----
@@ -754,47 +732,37 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     // the matrix pipe instead of after it. With two tiles the chains
     // alternate, each keeping its own k order.
     v4f acc[kTiles];
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+    acc[0] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
     const float* aw = As + li * kLd + 4 * g;
-    const float* bw = Bs + (16 * kTiles * wave + li) * kLd + 4 * g;
-    // Software pipelined: chunk c + 1's operands are read from LDS before
+    // Software pipelined: chunk c + 1's A operands are read from LDS before
     // chunk c's MFMAs issue, so their latency hides behind that chunk's
-    // dependent MFMA chain (k order unchanged).
+    // dependent MFMA chain (k order unchanged). B comes from registers.
     v4f af_next = *reinterpret_cast<const v4f*>(aw);
-    v4f bf_next[kTiles];
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) bf_next[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd);
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
       if (c < chunks) {
         const v4f af = af_next;
-        v4f bf[kTiles];
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) bf[t] = bf_next[t];
-        if (c + 1 < chunks) {
-          af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
-#pragma unroll
-          for (int t = 0; t < kTiles; ++t) {
-            bf_next[t] = *reinterpret_cast<const v4f*>(bw + 16 * t * kLd + 16 * (c + 1));
-          }
-        }
-        // (the scheduler would otherwise sink those reads to their use)
+        if (c + 1 < chunks) af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
+        // (the scheduler would otherwise sink that read to its use)
         __builtin_amdgcn_sched_barrier(0);
+        float bf[4];
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[t].x, acc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf[t].y, acc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[t].z, acc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[t].w, acc[t], 0, 0, 0);
+        for (int st = 0; st < 4; ++st) {
+          // rows past K hold row K - 1: zero them (A is zero there, and
+          // 0 * inf would not be)
+          bf[st] = (CHUNKS > 0 || 16 * c + 4 * g + st < K) ? bq[c][st] : 0.0F;
+        }
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[0], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf[1], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[2], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[3], acc[0], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (kDeferred) {
         if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
       }
     }
+    if (s + 1 < s1 && cur.e != si.e) load_b(cur.e);  // the next strip's segment
     if constexpr (kDeferred) {
       // (rows 0..3 of the previous strip went out at c = 3, 7, 11, 15: the
       // calls sit outside the c < chunks test, so short K emits them too)
@@ -901,7 +869,7 @@ int bn_for(int n) { return n <= 64 ? 64 : 128; }
 // Dynamic LDS bytes of one launch.
 std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   const int chunks = (K + 15) >> 4;
-  const std::size_t stage = static_cast<std::size_t>(bn + kRows) * (chunks * 16 + 4);
+  const std::size_t stage = static_cast<std::size_t>(kRows) * (chunks * 16 + 4);  // A rows (B: registers)
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
