@@ -334,8 +334,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // ---- B of a segment: this wave's 16 columns, whole K, in registers ----
   // bq[c][s] = B[16c + 4g + s][16 wave + li]: sixteen lanes read 64
   // contiguous bytes of one k row, a load instruction four rows. Columns past
-  // N read column N - 1 (their outputs are never stored); rows past K read row
-  // K - 1 and are zeroed where they are used.
+  // N read column N - 1 (their outputs are never stored); rows past K are
+  // zero (lanes masked off the load keep the zero: no wait for the data).
   float bq[kMaxChunks][4];
   auto load_b = [&](int e) {
     const float* W = p.W + static_cast<std::size_t>(e) * K * N;
@@ -346,8 +346,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       if (c < chunks) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int k = 16 * c + 4 * g + s;
-          bq[c][s] = W[(k < K ? k : K - 1) * N + nc];  // (K * N < 2^31: K <= 256, N <= 128)
+          const int k = 16 * c + 4 * g + s;  // (k * N < 2^31: K <= 256, N <= 128)
+          if constexpr (CHUNKS > 0) {
+            bq[c][s] = W[k * N + nc];  // K = 16 CHUNKS exactly
+          } else {
+            float v = 0.0F;
+            if (k < K) v = W[k * N + nc];
+            bq[c][s] = v;
+          }
         }
       }
     }
@@ -671,9 +677,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   bool pending = false;
 
   // Issue order: the first strip's A rows, the route map's weight loads,
-  // then B. Memory operations complete in order, so the A stage waits for
-  // A and the weights alone, and the first strip's MFMAs wait for B one k
-  // chunk at a time.
+  // B, then the route map's stores. Memory operations complete in order, so
+  // the A stage waits for A and the weights alone, and the first strip's
+  // MFMAs wait for B one k chunk at a time. At K > 224 B is more loads per
+  // lane (4 per k chunk) than a wave may have outstanding (63): the wave
+  // stalls at issue until B starts to arrive, so B then follows the route
+  // map's stores instead (measured at K = 256: expert launch 18.6 us against
+  // 19.6 us; at K = 128 B before the stores is faster).
   int src = -1;
   if (s0 < s1) {
     src = a_source(s0, cur);
@@ -682,19 +692,24 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   if constexpr (MODE == kStripChain) {
     // Route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows.
-    if (tid < (s1 - s0) * kRows) {  // <= (kMaxSegs + 1) * 16 <= kThreads
+    const bool b_early = 4 * chunks < 60;
+    const bool mine = tid < (s1 - s0) * kRows;  // <= (kMaxSegs + 1) * 16 <= kThreads
+    const int32_t route = mine ? s_slot[tid] : -1;
+    if (route >= 0 && p.combine) w_pending = p.route_weights[route];
+    if (s0 < s1 && b_early) load_b(cur.e);
+    if (mine) {
       // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
       const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
-      const int32_t route = s_slot[tid];
       s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
       if (route >= 0) {
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
-        if (p.combine) w_pending = p.route_weights[route];
       }
     }
+    if (s0 < s1 && !b_early) load_b(cur.e);
+  } else {
+    if (s0 < s1) load_b(cur.e);
   }
-  if (s0 < s1) load_b(cur.e);
   for (int s = s0; s < s1; ++s) {
     const StripInfo si = cur;
     __syncthreads();  // every wave is done with As
@@ -745,17 +760,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if (c + 1 < chunks) af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
         // (the scheduler would otherwise sink that read to its use)
         __builtin_amdgcn_sched_barrier(0);
-        float bf[4];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          // rows past K hold row K - 1: zero them (A is zero there, and
-          // 0 * inf would not be)
-          bf[st] = (CHUNKS > 0 || 16 * c + 4 * g + st < K) ? bq[c][st] : 0.0F;
-        }
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[0], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf[1], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[2], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[3], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bq[c][0], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bq[c][1], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bq[c][2], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bq[c][3], acc[0], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (kDeferred) {
