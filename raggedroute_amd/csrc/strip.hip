@@ -275,13 +275,11 @@ __device__ __forceinline__ StripInfo strip_info(const SegTable& t, int nblk, int
   return si;
 }
 
-// Waves per workgroup: one per 16-column tile (BN / 16). The kernel also
-// runs with fewer waves, each owning BN / 16 / waves adjacent tiles (two
-// independent MFMA chains): at BN = 128, four waves of two tiles measured
-// 26.6 us for the headline chain's expert launch against 22.6 us for eight
-// waves of one tile; two waves per SIMD hide the LDS and memory latencies
-// that one wave exposes. The router needs one tile per wave (its gate merge
-// runs per wave).
+// Waves per workgroup: one per 16-column tile (BN / 16), each holding its
+// tile's B in registers. (Four waves of two tiles each, tried at BN = 128
+// when B sat in LDS, measured 26.6 us for the headline chain's expert launch
+// against 22.6 us for eight waves of one tile: two waves per SIMD hide the
+// LDS and memory latencies that one wave exposes.)
 constexpr int kWaves128 = 8;
 constexpr int strip_waves(int bn, int mode) {
   return mode == kStripRouterGate ? bn / 16 : (bn == 128 ? kWaves128 : 4);
