@@ -242,6 +242,9 @@ def run_stages(cfg, inp, device, ctx):
     ("tokens", 5, 4, 7, 5), ("tokens", 512, 32, 256, 64), ("tokens", 4096, 64, 256, 128),
     ("tokens", 1000, 128, 96, 40), ("tokens", 777, 256, 64, 33), ("tokens", 300, 1024, 20, 12),
     ("logits", 4096, 64, 256, 128), ("logits", 333, 7, 13, 9), ("tokens", 50, 8, 16, 0),
+    # K tails of the strip kernel's register B: 16 chunks with masked rows
+    # (B issued after the route map), 14 chunks (before it)
+    ("tokens", 700, 64, 252, 128), ("logits", 900, 32, 224, 96),
 ])
 @pytest.mark.parametrize("with_inverse", [True, False])
 def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):

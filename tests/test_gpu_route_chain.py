@@ -144,10 +144,12 @@ def test_route_chain_release_shapes(ctx, device, name, distribution):
 
 @pytest.mark.parametrize("shape", [(1, 1, 1, 4, 4), (33, 5, 3, 12, 9), (300, 1024, 8, 20, 12),
                                    (2000, 128, 4, 260, 40), (700, 256, 2, 64, 130), (9, 6, 2, 0, 8),
-                                   (9, 6, 2, 8, 0)])
+                                   (9, 6, 2, 8, 0), (600, 64, 2, 252, 128), (500, 32, 4, 228, 64)])
 def test_route_chain_edge_shapes(ctx, device, shape):
     """E = top_k = 1, odd K / N (no vector path), E = 1024, K above the strip
-    limit (route_prep + tiled gathered GEMM), N above it, K = 0 and N = 0."""
+    limit (route_prep + tiled gathered GEMM), N above it, K = 0 and N = 0,
+    and K tails of the strip kernel's register B (252: masked rows in the
+    last k chunk; 228: fifteen chunks)."""
     t, e, top, k, n = shape
     cfg = workloads.RouteChainConfig("edge", t, e, k, n, top, "uniform")
     inp = workloads.route_chain_inputs(cfg, seed=13)
