@@ -38,6 +38,7 @@ def tile_env():
 GROUPED = [
     ([0, 300, 5, 1000, 0, 0, 77, 1], 256, 128, 0),  # strip-eligible default
     ([0, 300, 5, 1000, 0, 0, 77, 1], 100, 72, 0),
+    ([0, 300, 5, 1000, 0, 0, 77, 1], 252, 128, 0),  # strip K tail: masked rows of the last k chunk
     ([7, 0, 12, 1, 0], 33, 17, 0),                    # scalar loads (K, N odd)
     ([40, 0, 3, 90], 96, 40, 1),                      # offset pointers
     ([200, 129, 64], 300, 136, 0),                    # K past 256, N past 128
@@ -61,7 +62,8 @@ def test_grouped_tiles_bit_identical(ctx, device, tile_env, counts, k, n, offset
         assert np.array_equal(y.view(np.uint32), base.view(np.uint32)), tile
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 64, 256), (300, 128, 96), (77, 40, 260), (129, 17, 33)])
+@pytest.mark.parametrize("m,n,k", [(4096, 64, 256), (300, 128, 96), (500, 128, 244), (77, 40, 260),
+                                   (129, 17, 33)])
 def test_dense_tiles_bit_identical(ctx, device, tile_env, m, n, k):
     import torch
     from conftest import to_dev, to_host
