@@ -599,12 +599,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // (t % kRowThreads) + kRowThreads u (row-contiguous across the threads).
   const int a_row = tid / kRowThreads;
   const int a_col = tid % kRowThreads;
+  // token of a route (route = top_k * token + rank, route >= 0): a shift for
+  // the top-2 chains instead of an integer division
+  auto token_of = [&](int32_t route) -> int32_t {
+    return p.top_k == 2 ? (route >> 1) : route / p.top_k;
+  };
   auto a_source = [&](int s, const StripInfo& si) -> int {
     if constexpr (MODE == kStripChain) {
       (void)si;
       if (s == s0) {  // before the loop: s_tok is written after the last barrier
         const int32_t route = s_slot[a_row];
-        return route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
+        return route >= 0 ? token_of(route) : -1;
       }
       return s_tok[(s - s0) * kRows + a_row];
     } else {
@@ -698,7 +703,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     if (mine) {
       // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
       const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
-      s_tok[tid] = route >= 0 ? route / p.top_k : -1;  // route = top_k * token + rank
+      s_tok[tid] = route >= 0 ? token_of(route) : -1;
       if (route >= 0) {
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
