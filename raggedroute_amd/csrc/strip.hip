@@ -305,9 +305,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   const int nblk = (E + 63) >> 6;
   const int chunks = CHUNKS > 0 ? CHUNKS : (K + 15) >> 4;
   const int kLd = chunks * 16 + 4;
-  float* As = lds;                // [16][kLd]: A rows of the current strip
+  float* As2 = lds;               // [2][16][kLd]: A rows of strip s in buffer s & 1
   constexpr int kLgLd = BN + 4;       // router: padded row of the logit tile
-  float* s_lg = As + kRows * kLd;      // router: [16][kLgLd] logits of the strip
+  float* s_lg = As2 + 2 * kRows * kLd;  // router: [16][kLgLd] logits of the strip
   // chain: [waves][kMaxSegs][4] segment lists (16-byte aligned)
   int32_t* s_seglist = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 4 : 0);  // chain: [max_strips * 16]
@@ -715,7 +715,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   }
   for (int s = s0; s < s1; ++s) {
     const StripInfo si = cur;
-    __syncthreads();  // every wave is done with As
+    // No barrier before the A store: buffer s & 1 was last read by strip
+    // s - 2's MFMAs, which every wave finished before the barrier below in
+    // strip s - 1 (and the router's logit tile is rewritten only after that
+    // barrier too).
+    float* As = As2 + (s & 1) * kRows * kLd;
     // ---- this strip's A rows -> LDS (zeros past K up to the chunk edge) ----
 #pragma unroll
     for (int u = 0; u < kALoads; ++u) {
@@ -880,7 +884,7 @@ int bn_for(int n) { return n <= 64 ? 64 : 128; }
 // Dynamic LDS bytes of one launch.
 std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   const int chunks = (K + 15) >> 4;
-  const std::size_t stage = static_cast<std::size_t>(kRows) * (chunks * 16 + 4);  // A rows (B: registers)
+  const std::size_t stage = 2 * static_cast<std::size_t>(kRows) * (chunks * 16 + 4);  // A rows, two buffers (B: registers)
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
