@@ -13,8 +13,9 @@
 //     transposing stores and no barrier, and the first strip's MFMAs wait for
 //     each k chunk of B as it arrives rather than for all of it.
 //   A rows (16 x K) are loaded by the whole workgroup with row-contiguous
-//     float4 accesses into registers, stored to a [16][K + 4] LDS stage, and
-//     the next strip's rows are loaded while the current strip's MFMAs run.
+//     float4 accesses into registers, stored to one of two [16][K + 4] LDS
+//     stages (strips alternate, one barrier per strip), and the next strip's
+//     rows are loaded while the current strip's MFMAs run.
 // Accumulation order per output element: k chunks of 16 ascending, inside a
 // chunk MFMA step s sums k = 16c + 4g + s over g = 0..3, exactly as the tiled
 // kernel in gemm.hip does, so both produce bit-identical results.
