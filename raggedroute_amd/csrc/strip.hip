@@ -407,10 +407,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     for (int u = 0; u < kIdChunks; ++u) {
       if (c_begin + u < c_end) {
         const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
+        const int r = (c_begin + u) * 256 + 4 * lane;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           if (static_cast<unsigned>(vals[k]) < static_cast<unsigned>(E)) {
             atomicAdd(s_cntw + wave * 64 * nblk + vals[k], 1);  // this wave's own row
+          } else if (b == 0 && r + k < R) {
+            // a route whose id lies outside [0, E) is never placed: its map
+            // entry says so (workgroup 0 alone holds the write)
+            p.route_pos[r + k] = -1;
           }
         }
       }

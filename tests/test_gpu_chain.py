@@ -350,3 +350,48 @@ def test_router_gate_sweep(ctx, device, experts):
     assert np.array_equal(ids, e_ids)
     fails, max_abs, _ = oracle.compare_floating(w, e_w, 1e-6, 1e-6)
     assert fails == 0, max_abs
+
+
+@pytest.mark.parametrize("shape", [(512, 16, 64, 64), (700, 32, 300, 40)])
+def test_fused_combine_subnormal_products(ctx, device, shape):
+    """The fused combine adds w * y_permuted into y with hardware FP32 atomics;
+    the stage-by-stage unpermute sums with plain FP32 operations. With
+    y_permuted entries just above the smallest normal (2^-126 (1 + u)) and
+    weights below one, most products w * y_permuted are subnormal: the fused
+    y must still equal the staged y and the host's IEEE FP32 rank-order sum
+    bit for bit (subnormals kept, not flushed). Merged strip launch (K <= 256)
+    and the tiled GEMM's combine (K > 256)."""
+    t, e, k, n = shape
+    cfg = workloads.ChainConfig("subnormal", t, e, k, n, from_tokens=False)
+    inp = workloads.chain_inputs(cfg, seed=29)
+    x = np.zeros((t, k), np.float32)
+    x[np.arange(t), np.arange(t) % k] = np.float32(2.0 ** -63)  # one non-zero per row
+    u = workloads.unit_doubles(e * k * n, 29, workloads.S_EXPERTS).reshape(e, k, n)
+    we = (np.float32(2.0 ** -63) * (1.0 + u)).astype(np.float32)  # products x * W are normal
+    inp = dict(inp, x=x, expert_weights=we)
+    print(f"fused combine subnormal products {shape}", flush=True)
+    fused = ChainRun(cfg, inp, device).run(ctx)
+    ref = run_stages(cfg, inp, device, ctx)
+    yp, w, pos = fused["y_permuted"], fused["weights"], fused["route_pos"].reshape(t, 2)
+    prods = w[:, :, None] * yp[pos]
+    tiny = np.finfo(np.float32).tiny
+    assert ((prods != 0) & (np.abs(prods) < tiny)).mean() > 0.5, "products are not mostly subnormal"
+    want = (np.float32(0) + prods[:, 0]) + prods[:, 1]
+    assert np.array_equal(ref["y"].view(np.uint32), want.view(np.uint32)), "staged unpermute flushed subnormals"
+    assert np.array_equal(fused["y"].view(np.uint32), ref["y"].view(np.uint32)), \
+        "fused combine differs from the staged unpermute on subnormal products"
+
+
+@pytest.mark.parametrize("experts,output", [(64, 128), (128, 96)])
+def test_chain_router_four_strips_per_workgroup(ctx, device, experts, output):
+    """T=16384 with K=256: the router launch gives every workgroup four 16-token
+    strips, so both A buffers and the logit tile are reused (strip s takes
+    the buffer of strip s - 2); ids, weights and the route map in full, the
+    output on a seeded sample of 256 tokens."""
+    cfg = workloads.ChainConfig("router4", 16384, experts, 256, output, from_tokens=True)
+    inp_dev = workloads.chain_inputs_device(cfg, 0, device)
+    dev = ChainRun(cfg, inp_dev, device).run(ctx)
+    inp = {key: to_host(v) for key, v in inp_dev.items()}
+    sample = np.sort(workloads.seeded_permutation(cfg.tokens, 0, 78)[:256])
+    report = check_chain(cfg, inp, dev, sample_tokens=sample)
+    print(f"router four strips: {report}")

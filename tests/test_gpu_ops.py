@@ -68,6 +68,8 @@ def test_dense_gemm_kat(ctx, guarded, kat, kernel):
     (300, 64, 255, 0),     # K tail
     (1000, 128, 2048, 0),  # C5-shaped slice
     (129, 72, 96, 1),
+    (16384, 64, 256, 0),   # strip kernel: four 16-row strips per workgroup (A stage reused)
+    (16500, 128, 192, 0),  # ... and a ragged last strip
 ])
 @pytest.mark.parametrize("kernel", [NATIVE, NAIVE])
 def test_dense_gemm_random(ctx, guarded, m, n, k, offset, kernel):

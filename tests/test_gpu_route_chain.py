@@ -245,3 +245,60 @@ def test_route_chain_repeats_bit_for_bit(ctx, device, shape):
         for key, v in first.items():
             a, b = (again[key].view(np.uint32), v.view(np.uint32)) if v.dtype == np.float32 else (again[key], v)
             assert np.array_equal(a, b), key
+
+
+@pytest.mark.parametrize("shape", [(512, 64, 2, 128, 128), (2048, 32, 4, 64, 64), (1000, 128, 4, 300, 40)])
+def test_route_chain_invalid_ids(ctx, device, shape):
+    """Ids outside [0, E) (negative, E, E + 5) are never placed: they leave the
+    counts, route_pos says -1 for them even where it held a valid index
+    before the call, and y sums the valid routes of a token in rank order.
+    Both launch plans (one merged strip launch; route_prep + tiled GEMM)."""
+    t, e, top, k, n = shape
+    r = t * top
+    cfg = workloads.RouteChainConfig("invalid", t, e, k, n, top, "zipf")
+    inp = workloads.route_chain_inputs(cfg, seed=23)
+    ids = inp["ids"].reshape(-1).copy()
+    rng = np.random.default_rng(5)
+    bad = rng.choice(r, max(1, r // 20), replace=False)
+    ids[bad] = rng.choice(np.array([-1, -9, e, e + 5], np.int32), bad.size)
+    inp = dict(inp, ids=ids.reshape(t, top))
+    print(f"route chain invalid ids {shape}", flush=True)
+    run = RouteChainRun(cfg, inp, device)
+    run.pos.fill_(0)  # a valid index: an entry the call leaves alone would stay 0
+    dev = run.run(ctx)
+
+    valid = (ids >= 0) & (ids < e)
+    counts = np.bincount(ids[valid], minlength=e).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    assert np.array_equal(dev["counts"], counts)
+    assert np.array_equal(dev["offsets"], offsets)
+    want_pos = np.full(r, -1, np.int32)
+    seen = offsets[:-1].copy()
+    for route in range(r):  # stable order: route index ascending inside each expert
+        if valid[route]:
+            want_pos[route] = seen[ids[route]]
+            seen[ids[route]] += 1
+    assert np.array_equal(dev["route_pos"], want_pos), "route_pos differs (invalid routes must read -1)"
+    placed = np.nonzero(valid)[0]
+    assert np.array_equal(dev["sorted_route"][want_pos[placed]], placed)
+    token = np.arange(r) // top
+    assert np.array_equal(dev["x_permuted"][want_pos[placed]].view(np.uint32),
+                          inp["x"][token[placed]].view(np.uint32))
+    x64, we64 = inp["x"].astype(np.float64), inp["expert_weights"].astype(np.float64)
+    gamma = k * U32 / (1 - k * U32)
+    for ex in np.unique(ids[valid]):
+        routes = np.nonzero(ids == ex)[0]
+        xs = x64[token[routes]]
+        exact = xs @ we64[ex]
+        bound = 4 * gamma * (np.abs(xs) @ np.abs(we64[ex])) + 1e-7
+        assert (np.abs(dev["y_permuted"][want_pos[routes]].astype(np.float64) - exact) <= bound).all()
+    # y: rank-order FP32 sum from zero over the token's valid routes
+    w = inp["weights"].reshape(-1).astype(np.float32)
+    want_y = np.zeros((t, n), np.float32)
+    for j in range(top):
+        routes = np.arange(t) * top + j
+        ok_r = valid[routes]
+        term = np.zeros((t, n), np.float32)
+        term[ok_r] = w[routes[ok_r], None] * dev["y_permuted"][want_pos[routes[ok_r]]]
+        want_y = np.where(ok_r[:, None], want_y + term, want_y)
+    assert np.array_equal(dev["y"].view(np.uint32), want_y.view(np.uint32)), "y differs"
