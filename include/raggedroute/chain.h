@@ -2,6 +2,16 @@
 // and chain_from_logits only as benchmark suites (reference
 // benchmarks/adapters/chain_adapter.cpp:263-467); this build adds them as
 // library entries that enqueue every stage on the caller's stream.
+//
+// Memory contract of `y` (auto / optimized family): the fused chain zeroes y
+// in its first launch and adds both weighted routes of each token into it
+// with hardware FP32 atomic adds. y must be device memory of the GPU that runs
+// the chain, from hipMalloc or an allocator built on it (coarse-grained). Not
+// supported for y on that path: fine-grained device memory, host memory
+// (hipHostMalloc, registered, managed) and peer memory mapped over xGMI. Use
+// KernelFamily::kNaive or chain_from_route_ids (plain stores) for those. Every
+// element gets exactly two adds into zero, so the result is deterministic and
+// bit-identical to the rank-order unpermute, subnormal products included.
 #pragma once
 
 #include <cstddef>

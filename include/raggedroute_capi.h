@@ -341,7 +341,13 @@ rr_status rr_grouped_gemm(const rr_grouped_gemm_args* args, const rr_runtime_con
 rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* context);
 
 /* Chain entries: no reference counterpart as functions; they run the stage
- * sequence of reference benchmarks/adapters/chain_adapter.cpp:263-467. */
+ * sequence of reference benchmarks/adapters/chain_adapter.cpp:263-467.
+ * Auto / optimized family: y is zeroed by the first launch and both weighted
+ * routes of a token are added into it with hardware FP32 atomic adds, so y
+ * must be coarse-grained device memory of the running GPU (hipMalloc or an
+ * allocator on it); fine-grained, host, managed or peer-mapped memory is not
+ * supported for y there (use RR_FAMILY_NAIVE). Two adds into zero per
+ * element: deterministic, equal to the rank-order unpermute bit for bit. */
 rr_status rr_chain_from_tokens(const rr_chain_args* args, const rr_runtime_context* context);
 rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_context* context);
 /* No reference counterpart as a function: the stage sequence of the
