@@ -409,6 +409,21 @@ rr_status rr_chain_graph_cache_launch(rr_chain_graph_cache* cache, int32_t entry
 void rr_chain_graph_cache_get_stats(const rr_chain_graph_cache* cache, rr_chain_graph_cache_stats* stats);
 void rr_chain_graph_cache_destroy(rr_chain_graph_cache* cache);
 
+/* Static device scratch of rr_chain_from_tokens_noalloc: one copy per GPU,
+ * held until the process ends. */
+#define RR_CHAIN_NOALLOC_SCRATCH_BYTES (1u << 20)
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): rr_chain_from_tokens with the chain workspace taken from a fixed
+ * RR_CHAIN_NOALLOC_SCRATCH_BYTES device array instead of context->workspace
+ * (whose fields are ignored; stream and architecture are used). Shapes with
+ * rr_chain_workspace_size(args) > RR_CHAIN_NOALLOC_SCRATCH_BYTES (experts +
+ * 2 * tokens > 262144) are rejected with RR_STATUS_INVALID_ARGUMENT before any
+ * device call. Calls no allocating routine. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (several streams or threads) race
+ * on it. Outputs equal rr_chain_from_tokens's bit for bit. */
+rr_status rr_chain_from_tokens_noalloc(const rr_chain_args* args, const rr_runtime_context* context);
+
 /* No reference counterpart: timing hook. Runs one launch of the fused
  * (auto / optimized) chain alone so that a profiler or benchmark can time it
  * with events on the context's stream. Launches are numbered in execution

@@ -121,6 +121,12 @@ def chain_from_tokens(args: ChainArgs, context: RuntimeContext | None = None) ->
     return lib.rr_chain_from_tokens(byref(args), byref(_ctx(context)))
 
 
+def chain_from_tokens_noalloc(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
+    """chain_from_tokens with the workspace in the library's static device
+    scratch (context.workspace is ignored)."""
+    return lib.rr_chain_from_tokens_noalloc(byref(args), byref(_ctx(context)))
+
+
 def chain_from_logits(args: ChainArgs, context: RuntimeContext | None = None) -> Status:
     return lib.rr_chain_from_logits(byref(args), byref(_ctx(context)))
 

@@ -345,6 +345,7 @@ for _name, _args in _OP_ENTRIES:
 PROTOTYPES += [
     ("rr_chain_workspace_size", c_size_t, [POINTER(ChainArgs)]),
     ("rr_chain_from_tokens", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
+    ("rr_chain_from_tokens_noalloc", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_from_logits", Status, [POINTER(ChainArgs), POINTER(RuntimeContext)]),
     ("rr_chain_fused_launch", Status, [POINTER(ChainArgs), POINTER(RuntimeContext), c_int32, c_int32]),
     ("rr_chain_from_route_ids", Status, [POINTER(RouteChainArgs), POINTER(RuntimeContext)]),
