@@ -503,9 +503,8 @@ def trace_replay(torch, device, path=None, hidden=256, output=128, reps=100):
         tmp = tempfile.TemporaryDirectory()
         frames = {d.replace("zipf", "zipf1.4"): workloads.topk_route_ids(4096, 2, 64, d, seed=i)
                   for i, d in enumerate(("uniform", "zipf", "round_robin", "single_hot"))}
-        doc = route_trace.document("generated_t4096_e64", "synthetic_fixture", 64, frames)
         path = Path(tmp.name) / "generated.rrtrace"
-        path.write_text(route_trace.normalized_text(doc))
+        route_trace.write(path, "generated_t4096_e64", "synthetic_fixture", 64, frames)
     out = {}
     stream = torch.cuda.current_stream(device).cuda_stream
     for tr in route_trace.read_all(path):

@@ -359,12 +359,15 @@ rr_status rr_chain_from_logits(const rr_chain_args* args, const rr_runtime_conte
  * tolerance (atol 1e-4, rtol 4e-5 * K * top_k, :381). */
 rr_status rr_chain_from_route_ids(const rr_route_chain_args* args,
                                   const rr_runtime_context* context);
-/* reference include/raggedroute/benchmark/adapter_utils.h:269-322
- * (load_route_trace_frame): validates the whole trace file at `path` and
- * copies frame `frame`'s tokens * top_k expert ids (token-major, host memory)
- * into expert_ids; expert_ids = NULL reads the header only. The reference's
- * std::invalid_argument cases return RR_STATUS_INVALID_ARGUMENT with the same
- * message (without the path). Host-only: no device call. */
+/* Replaces reference include/raggedroute/benchmark/adapter_utils.h:269-322
+ * (load_route_trace_frame, behind --param route_trace_path / route_trace_frame).
+ * Reads the .rrtrace text v1 file at `path` (layout: schema tag, trace id,
+ * source kind, "T E top_k frames", then per frame its id and T * top_k expert
+ * ids), checks every frame and copies frame `frame`'s ids (token-major, host
+ * memory) into expert_ids only once the whole file checked out; expert_ids =
+ * NULL fills `info` alone. A file that breaks the format, or a frame index past
+ * the last, returns RR_STATUS_INVALID_ARGUMENT with a static message naming
+ * the rule. Host-only: no device call. */
 rr_status rr_route_trace_read(const char* path, int32_t frame, rr_route_trace_info* info,
                               int32_t* expert_ids, size_t capacity);
 /*

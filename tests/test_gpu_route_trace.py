@@ -33,9 +33,8 @@ def generated_trace(tmp_path, tokens=4096, experts=64, top_k=2):
         "round_robin": workloads.topk_route_ids(tokens, top_k, experts, "round_robin", seed=3),
         "single_hot": workloads.topk_route_ids(tokens, top_k, experts, "single_hot", seed=4),
     }
-    doc = route_trace.document("generated_t4096", "synthetic_fixture", experts, frames)
     path = tmp_path / "generated.rrtrace"
-    path.write_text(route_trace.normalized_text(doc))
+    route_trace.write(path, "generated_t4096", "synthetic_fixture", experts, frames)
     return path, frames
 
 

@@ -1,13 +1,11 @@
 """Route traces on the host: the native `.rrtrace` reader (rr_route_trace_read)
-against the reference's fixture and planted format errors (reference
-include/raggedroute/benchmark/adapter_utils.h:269-322), and the JSON form's
-validator / normaliser (reference scripts/validate_route_trace.py). CPU only.
+against the reference's fixture (configs/workloads/synthetic_fixture.rrtrace,
+transcribed into tests/golden) and planted format errors, and the writer's
+round trip. CPU only.
 """
 from __future__ import annotations
 
 import ctypes
-import hashlib
-import json
 from pathlib import Path
 
 import numpy as np
@@ -51,24 +49,28 @@ GOOD = FIXTURE.read_text()
 
 
 @pytest.mark.parametrize("mutate,message", [
-    (lambda s: s.replace("raggedroute.route_trace.v1", "raggedroute.route_trace.v2"), "header"),
-    (lambda s: s.replace("synthetic_fixture_t8_e8_top2", "bad id!"), "metadata"),
-    (lambda s: s.replace("\nsynthetic_fixture\n", "\nsynthetic\n"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "0 8 2 3"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "8 0 2 3"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "8 1025 2 3"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "8 8 9 3"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "8 8 2 0"), "metadata"),
-    (lambda s: s.replace("8 8 2 3", "8 8 2"), "header"),
-    (lambda s: s.replace("skewed", "balanced"), "frame id"),
+    (lambda s: s.replace("raggedroute.route_trace.v1", "raggedroute.route_trace.v2"), "line 1"),
+    (lambda s: s.replace("synthetic_fixture_t8_e8_top2", "bad id!"), "line 2"),
+    (lambda s: s.replace("\nsynthetic_fixture\n", "\nsynthetic\n"), "line 3"),
+    (lambda s: s.replace("8 8 2 3", "0 8 2 3"), "shape out of range"),
+    (lambda s: s.replace("8 8 2 3", "8 0 2 3"), "shape out of range"),
+    (lambda s: s.replace("8 8 2 3", "8 1025 2 3"), "shape out of range"),
+    (lambda s: s.replace("8 8 2 3", "8 8 9 3"), "shape out of range"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2 0"), "shape out of range"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2"), "line 4"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2 3 1"), "line 4"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2 x"), "line 4"),
+    (lambda s: s.replace("skewed", "balanced"), "share a frame id"),
     (lambda s: s.replace("skewed", "sk/ewed"), "frame id"),
-    (lambda s: s.replace("balanced 0 1", "balanced 0 8"), "expert id"),
-    (lambda s: s.replace("balanced 0 1", "balanced -1 1"), "expert id"),
-    (lambda s: s.replace("balanced 0 1", "balanced 0 x"), "expert id"),
-    (lambda s: s.replace("balanced 0 1", "balanced 1 1"), "repeats an expert"),
-    (lambda s: s.replace("shifted 7 6", "shifted 7 7"), "repeats an expert"),
-    (lambda s: s + "extra\n", "trailing"),
-    (lambda s: s.rsplit(" ", 1)[0] + "\n", "expert id"),
+    (lambda s: s.replace("balanced 0 1", "balanced 0 8"), "outside"),
+    (lambda s: s.replace("balanced 0 1", "balanced -1 1"), "outside"),
+    (lambda s: s.replace("balanced 0 1", "balanced 0 x"), "non-integer"),
+    (lambda s: s.replace("balanced 0 1", "balanced 0 1.0"), "non-integer"),
+    (lambda s: s.replace("balanced 0 1", "balanced 1 1"), "twice"),
+    (lambda s: s.replace("shifted 7 6", "shifted 7 7"), "twice"),
+    (lambda s: s + "extra\n", "follows the last frame"),
+    (lambda s: s.rsplit(" ", 1)[0] + "\n", "ends early"),
+    (lambda s: "", "line 1"),
 ])
 def test_reader_rejects_planted_errors(tmp_path, mutate, message):
     bad = mutate(GOOD)
@@ -77,12 +79,22 @@ def test_reader_rejects_planted_errors(tmp_path, mutate, message):
         route_trace.read(_write(tmp_path, bad), 0)
 
 
+def test_reader_accepts_layout_variants(tmp_path):
+    """CRLF line ends, records wrapped over several lines and a missing final
+    newline read the same ids as the fixture."""
+    variants = [GOOD.replace("\n", "\r\n"), GOOD.replace(" 4 5 ", "\n4 5\n "), GOOD.rstrip("\n")]
+    for i, text in enumerate(variants):
+        path = _write(tmp_path, text, f"v{i}.rrtrace")
+        for index in range(3):
+            assert np.array_equal(route_trace.read(path, index).ids, route_trace.read(FIXTURE, index).ids)
+
+
 def test_reader_argument_errors(tmp_path):
-    with pytest.raises(ValueError, match="cannot open"):
+    with pytest.raises(ValueError, match="cannot be opened"):
         route_trace.read(tmp_path / "missing.rrtrace", 0)
-    with pytest.raises(ValueError, match="metadata"):
-        route_trace.read(FIXTURE, 3)  # frame past the last
-    with pytest.raises(ValueError, match="invalid"):
+    with pytest.raises(ValueError, match="past the last frame"):
+        route_trace.read(FIXTURE, 3)
+    with pytest.raises(ValueError, match="frame index >= 0"):
         route_trace.read(FIXTURE, -1)
 
 
@@ -94,46 +106,47 @@ def test_error_in_a_later_frame_leaves_the_buffer_untouched(tmp_path):
     assert st.code == rr.StatusCode.kInvalidArgument and (buf == -5).all()
 
 
-def test_json_round_trip_and_cli(tmp_path, kat, capsys):
+def test_write_reproduces_the_reference_fixture(tmp_path, kat):
+    """The writer lays the fixture's frames out byte for byte as the
+    reference's normalised fixture file, and the reader returns them."""
     raw = kat.raw["route_trace_fixture"]
-    doc = route_trace.document(raw["trace_id"], raw["source_kind"], raw["experts"],
-                               {f: np.array(raw["frames"][f]).reshape(8, 2) for f in FRAMES})
-    assert route_trace.normalized_text(doc) == GOOD  # byte-identical to the reference fixture
-    src = tmp_path / "trace.json"
-    src.write_text(json.dumps(doc))
-    out = tmp_path / "norm" / "trace.rrtrace"
-    assert route_trace.main([str(src), "--output-normalized", str(out)]) == 0
-    summary = json.loads(capsys.readouterr().out)
-    assert summary["normalized_sha256"] == hashlib.sha256(GOOD.encode()).hexdigest()
-    assert summary["frames"] == 3 and out.read_text() == GOOD
+    frames = {f: np.array(raw["frames"][f]).reshape(8, 2) for f in FRAMES}
+    out = tmp_path / "fixture.rrtrace"
+    text = route_trace.write(out, raw["trace_id"], raw["source_kind"], raw["experts"], frames)
+    assert text == GOOD and out.read_text() == GOOD
     assert route_trace.read(out, 1).ids.reshape(-1).tolist() == raw["frames"]["skewed"]
-    with pytest.raises(ValueError, match="synthetic_fixture"):
-        route_trace.main([str(src), "--require-real"])
 
 
-@pytest.mark.parametrize("edit,message", [
-    (lambda d: d.update(extra=1), "unknown trace fields"),
-    (lambda d: d.update(schema_version="v0"), "schema_version"),
-    (lambda d: d.update(trace_id="a b"), "trace_id"),
-    (lambda d: d.update(source_kind="lab"), "source_kind"),
-    (lambda d: d.update(tokens=True), "tokens"),
-    (lambda d: d.update(experts=2000), "experts"),
-    (lambda d: d.update(top_k=9), "top_k"),
-    (lambda d: d.update(frames=[]), "frames"),
-    (lambda d: d["frames"][0].update(weight=1), "only frame_id and expert_ids"),
-    (lambda d: d["frames"][1].update(frame_id="balanced"), "duplicate frame_id"),
-    (lambda d: d["frames"][0].update(expert_ids=[0] * 15), "must contain 16"),
-    (lambda d: d["frames"][0]["expert_ids"].__setitem__(3, 8), "out-of-range"),
-    (lambda d: d["frames"][0]["expert_ids"].__setitem__(1, 0), "repeats an expert"),
+@pytest.mark.parametrize("top_k,experts", [(1, 1), (4, 64), (8, 1024)])
+def test_write_read_round_trip(tmp_path, top_k, experts):
+    from raggedroute_amd import workloads
+    frames = {f"f{i}.{d}": workloads.topk_route_ids(37, top_k, experts, d, seed=i)
+              for i, d in enumerate(("uniform", "zipf", "round_robin"))}
+    path = tmp_path / "rt.rrtrace"
+    route_trace.write(path, "gen_trace-1", "captured", experts, frames)
+    back = route_trace.read_all(path)
+    assert [t.frame_id for t in back] == list(frames)
+    for tr, ids in zip(back, frames.values()):
+        assert (tr.tokens, tr.top_k, tr.experts, tr.source_kind) == (37, top_k, experts, "captured")
+        assert np.array_equal(tr.ids, ids)
+
+
+@pytest.mark.parametrize("call,message", [
+    (lambda w: w("a b", "captured", 8, {"f": np.zeros((2, 1), int)}), "trace id"),
+    (lambda w: w("t", "lab", 8, {"f": np.zeros((2, 1), int)}), "source kind"),
+    (lambda w: w("t", "captured", 8, {}), "at least one frame"),
+    (lambda w: w("t", "captured", 2000, {"f": np.zeros((2, 1), int)}), "outside"),
+    (lambda w: w("t", "captured", 8, {"f/1": np.zeros((2, 1), int)}), "frame id"),
+    (lambda w: w("t", "captured", 8, {"a": np.zeros((2, 1), int), "b": np.zeros((3, 1), int)}), "one"),
+    (lambda w: w("t", "captured", 8, {"f": np.full((2, 1), 8)}), "in \\[0, 8\\)"),
+    (lambda w: w("t", "captured", 8, {"f": np.array([[1, 1]])}), "twice"),
+    (lambda w: w("t", "captured", 2, {"f": np.array([[0, 1, 2]])}), "in \\[0, 2\\)"),
 ])
-def test_json_validator_rejects(kat, edit, message):
-    raw = kat.raw["route_trace_fixture"]
-    doc = json.loads(json.dumps(route_trace.document(
-        raw["trace_id"], raw["source_kind"], raw["experts"],
-        {f: np.array(raw["frames"][f]).reshape(8, 2) for f in FRAMES})))
-    edit(doc)
+def test_writer_refuses_what_the_reader_would(tmp_path, call, message):
+    path = tmp_path / "never.rrtrace"
     with pytest.raises(ValueError, match=message):
-        route_trace.validate_trace(doc)
+        call(lambda *a: route_trace.write(path, *a))
+    assert not path.exists()
 
 
 def test_logits_for_ids_select_the_trace_ids(kat):
