@@ -1,15 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 routing chain (one MI355X).
 
-Headline: chain_from_tokens at T=4096, E=64, K=256, N=128 (FP32), value =
-tokens/s over exactly --steps chains bracketed by device synchronisation.
-Every stage is also timed on its own (HIP events on the launch stream,
-average over back-to-back launches) and priced against its roofline with the
-algorithmic work model (minimum unique traffic / GEMM flops). Extras measured
-in the same run: the Mixtral-shaped grouped GEMM + permute + unpermute (C4,
-aligned and non-aligned), the fine-grained chain (C5) and the histogram-scan
-stress (C3). The CPU baseline is the reference CPU oracle chain restated in
-oracle/ (single thread), timed on the host on the same headline workload.
+Headline: chain_from_tokens at T=4096, E=64, K=256, N=128 (FP32). After
+--warmup untimed chains, exactly --steps chains run in at most 20 batches;
+each batch is one HIP-event span divided by its size (reference runner
+semantics, benchmarks/core/runner.cpp:218-236, 283-411) and value = T / p50
+of the batch means. Each fused launch and each stage operator is also timed
+alone, 50 back-to-back calls recorded into one HIP graph (no host submission
+between them), and priced against its roofline with the algorithmic work
+model (minimum unique traffic / GEMM flops). Extras measured in the same run:
+the Mixtral-shaped grouped GEMM + permute + unpermute (C4, aligned and
+non-aligned; permute / unpermute warm and cold), the fine-grained chain (C5),
+the histogram-scan stress (C3, with the launch floor beside it), chain graphs
+of 1 / 10 / 50 chains against direct calls. The CPU baseline is the reference
+CPU oracle chain restated in oracle/ (single thread), timed on the host on the
+same headline workload.
+
+Runner mode (`--suite NAME` or `--operator NAME` with `--param key=value ...`,
+`--variant`, `--cache-mode warm|cold_scrub`, `--samples`, `--kernel-repeats`,
+`--profile-once`; reference benchmarks/benchmark_main.cpp:16-33) times any
+shape and prints one record of the same form.
 
 Prints one JSON line. `--gpus N` with N > 1 exits with a message: this build
 runs on one GPU.
@@ -17,6 +27,7 @@ runs on one GPU.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -34,19 +45,35 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor peak
 RIDGE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # flop/byte
 
 
-def parse():
+SUITES = ("chain_from_tokens", "chain_from_logits", "chain_from_route_ids")
+OPERATORS = ("dense_gemm", "topk_gate", "histogram", "exclusive_scan", "histogram_exclusive_scan",
+             "token_permute", "grouped_gemm", "unpermute")
+
+
+def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--stage-reps", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
     ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route,trace")
     ap.add_argument("--route-trace", default="", help="replay every frame of this .rrtrace file (extras.route_trace)")
-    ap.add_argument("--profile", default="", choices=["", "headline", "c4"],
+    ap.add_argument("--profile", default="", choices=["", "headline", "c4", "c3"],
                     help="profiler driver: a fixed number of launches of one case, no timing, "
                          "no JSON line (for rocprofv3 --pmc / --kernel-trace runs)")
-    return ap.parse_args()
+    # shape-generic runner (reference benchmarks/benchmark_main.cpp:16-33)
+    ap.add_argument("--suite", choices=SUITES, help="runner mode: time one chain entry at --param shapes")
+    ap.add_argument("--operator", choices=OPERATORS, help="runner mode: time one operator at --param shapes")
+    ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
+                    help="T, E, K, N, top_k, distribution, zipf_s, tie_fraction, seed")
+    ap.add_argument("--variant", default="auto", choices=["auto", "naive", "optimized"])
+    ap.add_argument("--cache-mode", default="warm", choices=["warm", "cold_scrub"])
+    ap.add_argument("--cache-scrub-bytes", type=int, default=512 << 20)
+    ap.add_argument("--samples", type=int, default=20)
+    ap.add_argument("--kernel-repeats", type=int, default=10)
+    ap.add_argument("--profile-once", action="store_true",
+                    help="runner mode: warm up, then enqueue one call without timing and print nothing")
+    return ap.parse_args(argv)
 
 
 # ------------------------------------------------------------------ work model
@@ -58,6 +85,8 @@ def work_model(t, e, k, n, active=None, sorted_route=False):
     return {
         "dense_gemm": (4 * (t * k + k * e + t * e), 2.0 * t * k * e),
         "topk_gate": (4 * t * e + 8 * r, 0.0),
+        "histogram": (4 * r + 4 * e, 0.0),
+        "exclusive_scan": (4 * e + 4 * (e + 1), 0.0),
         "histogram_scan": (4 * r + 4 * e + 4 * (e + 1), 0.0),
         "token_permute": (4 * t * k + 4 * r * k + 4 * r + 4 * (e + 1) + 4 * r + (4 * r if sorted_route else 0), 0.0),
         "grouped_gemm": (4 * (r * k + active * k * n + r * n) + 4 * (e + 1), 2.0 * r * k * n),
@@ -144,6 +173,10 @@ class Chain:
                                                            c=mv(ptr(self.logits)), m=t, n=e, k=k)),
             "topk_gate": (rr.topk_gate, rr.TopKGateArgs(logits=cv(ptr(self.logits)), expert_ids=ptr(self.ids),
                                                         weights=mv(ptr(self.w)), tokens=t, experts=e)),
+            "histogram": (rr.histogram, rr.HistogramArgs(
+                expert_ids=ptr(self.ids), counts=ptr(self.counts), route_pairs=2 * t, experts=e)),
+            "exclusive_scan": (rr.exclusive_scan, rr.ExclusiveScanArgs(
+                counts=ptr(self.counts), offsets=ptr(self.offsets), experts=e)),
             "histogram_scan": (rr.histogram_exclusive_scan, rr.HistogramExclusiveScanArgs(
                 expert_ids=ptr(self.ids), counts=ptr(self.counts), offsets=ptr(self.offsets),
                 route_pairs=2 * t, experts=e)),
@@ -160,27 +193,35 @@ class Chain:
         if not cfg.from_tokens:
             del self.stage_args["dense_gemm"]
 
-    def chain(self):
+    def ctx_on(self, stream):
+        """The chain's context on another HIP stream (handle)."""
+        return self.rr.RuntimeContext(stream=stream, workspace=self.ctx.workspace,
+                                      workspace_bytes=self.ctx.workspace_bytes,
+                                      architecture=self.ctx.architecture)
+
+    def chain(self, stream=None):
         fn = self.rr.chain_from_tokens if self.cfg.from_tokens else self.rr.chain_from_logits
-        status = fn(self.chain_args, self.ctx)
+        status = fn(self.chain_args, self.ctx if stream is None else self.ctx_on(stream))
         if not status.ok():
             raise RuntimeError(status.message)
 
-    def fused_launch(self, index):
-        status = self.rr.chain_fused_launch(self.chain_args, self.ctx, self.cfg.from_tokens, index)
+    def fused_launch(self, index, stream=None):
+        ctx = self.ctx if stream is None else self.ctx_on(stream)
+        status = self.rr.chain_fused_launch(self.chain_args, ctx, self.cfg.from_tokens, index)
         if not status.ok():
             raise RuntimeError(f"fused launch {index}: {status.message}")
 
-    def stage(self, name):
+    def stage(self, name, stream=None):
         fn, args = self.stage_args[name]
-        status = fn(args, self.ctx)
+        status = fn(args, self.ctx if stream is None else self.ctx_on(stream))
         if not status.ok():
             raise RuntimeError(f"{name}: {status.message}")
 
 
 def time_loop(torch, fn, reps, warmup=3):
     """Average seconds per call of `fn` over `reps` back-to-back launches,
-    bracketed by HIP events on the current stream."""
+    bracketed by HIP events on the current stream (host-submitted: use for
+    calls long enough that the GPU never waits for the host)."""
     for _ in range(warmup):
         fn()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -191,6 +232,30 @@ def time_loop(torch, fn, reps, warmup=3):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3 / reps
+
+
+def graph_time(torch, device, call, n=50, replays=4):
+    """Average seconds per call: `n` calls recorded back to back into one HIP
+    graph (torch.cuda.CUDAGraph) and the graph replayed `replays` times between
+    HIP events. No host submission sits between the calls, so short kernels
+    are timed at the GPU's rate. `call(stream)` enqueues one call on the HIP
+    stream handle it is given (kernels only: no memset or allocation)."""
+    stream = torch.cuda.Stream(device)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(n):
+            call(stream.cuda_stream)
+    graph.replay()  # (first replay uploads)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    stop.synchronize()
+    del graph
+    return start.elapsed_time(stop) / 1e3 / (replays * n)
 
 
 def percentile(values, q):
@@ -211,31 +276,89 @@ def sample_stats(seconds):
             "p95_us": round(percentile(seconds, 0.95) * 1e6, 2), "cv": round(cv, 4)}
 
 
-def batch_means(torch, fn, samples, repeats):
-    """Reference runner semantics (runner.cpp:283-411): each sample is one event
-    span over `repeats` back-to-back calls divided by `repeats`."""
-    out = []
-    for _ in range(samples):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(repeats):
+def batch_sizes(steps, samples=20):
+    """`steps` calls split into min(samples, steps) batches whose sizes differ
+    by at most one and sum to exactly `steps`."""
+    n = max(1, min(samples, steps))
+    return [steps // n + (1 if i < steps % n else 0) for i in range(n)]
+
+
+class Marks:
+    """Timing-only HIP events, created through the HIP runtime the process has
+    already loaded, with hipEventDisableSystemFence: recording one then skips
+    the system-scope cache writeback and invalidate of a default event, which
+    costs about 1.6 us of GPU time per event on MI355X (measured between
+    back-to-back headline chains: 26.8 us per chain with default events,
+    25.0 us with these, 23.9 us with no event in between)."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+    _hip = None
+
+    def __init__(self, count):
+        if Marks._hip is None:
+            path = next(line.split()[-1] for line in Path("/proc/self/maps").read_text().splitlines()
+                        if "libamdhip64" in line)
+            Marks._hip = ctypes.CDLL(path)
+        self.events = []
+        for _ in range(count):
+            ev = ctypes.c_void_p()
+            rc = Marks._hip.hipEventCreateWithFlags(ctypes.byref(ev), ctypes.c_uint(self.DISABLE_SYSTEM_FENCE))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            self.events.append(ev)
+
+    def record(self, i, stream):
+        if Marks._hip.hipEventRecord(self.events[i], ctypes.c_void_p(stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def synchronize(self, i):
+        if Marks._hip.hipEventSynchronize(self.events[i]) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+
+    def seconds(self, i, j):
+        ms = ctypes.c_float()
+        if Marks._hip.hipEventElapsedTime(ctypes.byref(ms), self.events[i], self.events[j]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value / 1e3
+
+    def __del__(self):
+        for ev in self.events:
+            Marks._hip.hipEventDestroy(ev)
+
+
+def batch_means(torch, fn, samples=20, repeats=10, sizes=None, stream=None):
+    """Reference runner semantics (runner.cpp:218-236, 283-411): each sample is
+    the event span of a batch of back-to-back calls divided by the batch size.
+    The batches run back to back too, separated only by timing-only events
+    (Marks), with one host synchronisation at the end; a short device spin
+    first lets the host queue the work ahead of the first event."""
+    sizes = sizes or [repeats] * samples
+    stream = torch.cuda.current_stream().cuda_stream if stream is None else stream
+    marks = Marks(len(sizes) + 1)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(200_000)  # ~0.1 ms of GPU time, before the first event
+    marks.record(0, stream)
+    for i, reps in enumerate(sizes):
+        for _ in range(reps):
             fn()
-        b.record()
-        b.synchronize()
-        out.append(a.elapsed_time(b) / 1e3 / repeats)
-    return out
+        marks.record(i + 1, stream)
+    marks.synchronize(len(sizes))
+    return [marks.seconds(i, i + 1) / reps for i, reps in enumerate(sizes)]
 
 
-def cold_spans(torch, ch, device, samples, scrub_mib=512):
-    """Single chains, each after a scrub of scrub_mib MiB written through the
-    caches (rr_launch_cache_scrub): the chain's working set (~60 MB) otherwise
-    stays in the 256 MB Infinity Cache between calls."""
+def cold_spans(torch, ch, device, samples, scrub_mib=512, call=None):
+    """Single calls (a chain by default), each after a scrub of scrub_mib MiB
+    written through the caches (rr_launch_cache_scrub): the chain's working set
+    (~60 MB) and C4's x (134 MB) otherwise stay in the 256 MB Infinity Cache
+    between calls. The scrub also keeps the GPU busy while the host queues the
+    timed call."""
+    call = call or ch.chain
     scrub = torch.empty(scrub_mib << 18, dtype=torch.int32, device=device)
     out = []
     for _ in range(samples):
         assert ch.rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), ch.stream) == 0
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(); ch.chain(); b.record()
+        a.record(); call(); b.record()
         b.synchronize()
         out.append(a.elapsed_time(b) / 1e3)
     del scrub
@@ -243,14 +366,14 @@ def cold_spans(torch, ch, device, samples, scrub_mib=512):
 
 
 def graph_report(torch, device, ch, reps=200):
-    """The headline chain replayed from a captured graph (rr_chain_graph_*)
-    against direct calls: GPU time per chain (events over `reps` back-to-back
-    calls on one stream) and host time to submit one call (no synchronisation
-    inside the loop)."""
+    """The chain replayed from captured graphs (rr_chain_graph_*) against
+    direct calls: GPU time per chain (events over back-to-back launches on one
+    stream) and host time to submit one chain (no synchronisation inside the
+    loop), for graphs of 1, 10 and 50 chains (a sequence graph: one
+    hipGraphLaunch replays them all)."""
     rr = ch.rr
     stream = torch.cuda.Stream(device)
-    ctx = rr.RuntimeContext(stream=stream.cuda_stream, workspace=ch.ctx.workspace,
-                            workspace_bytes=ch.ctx.workspace_bytes, architecture=ch.ctx.architecture)
+    ctx = ch.ctx_on(stream.cuda_stream)
     entry = rr.CHAIN_FROM_TOKENS if ch.cfg.from_tokens else rr.CHAIN_FROM_LOGITS
     fn = rr.chain_from_tokens if ch.cfg.from_tokens else rr.chain_from_logits
 
@@ -258,38 +381,49 @@ def graph_report(torch, device, ch, reps=200):
         status = fn(ch.chain_args, ctx)
         assert status.ok(), status.message
 
+    def submit_us(call, per_call, n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            call()
+        elapsed = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        return round(elapsed / (n * per_call) * 1e6, 2)
+
     out = {}
-    with rr.ChainGraph(entry, ch.chain_args, ctx) as graph, torch.cuda.stream(stream):
-        def replay():
-            status = graph.launch(stream.cuda_stream)
-            assert status.ok(), status.message
-        out["kernel_nodes"] = graph.kernel_nodes
-        for name, call in (("direct", direct), ("graph", replay)):
-            out[f"{name}_us"] = round(time_loop(torch, call, reps, warmup=10) * 1e6, 2)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                call()
-            out[f"{name}_submit_us"] = round((time.perf_counter() - t0) / reps * 1e6, 2)
-            torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out["direct_us"] = round(time_loop(torch, direct, reps, warmup=10) * 1e6, 2)
+        out["direct_submit_us"] = submit_us(direct, 1, reps)
+        for chains in (1, 10, 50):
+            with rr.ChainGraph(entry, [ch.chain_args] * chains if chains > 1 else ch.chain_args, ctx) as graph:
+                def replay():
+                    status = graph.launch(stream.cuda_stream)
+                    assert status.ok(), status.message
+                n = max(4, reps // chains)
+                key = f"graph{chains}"
+                out[f"{key}_kernel_nodes"] = graph.kernel_nodes
+                out[f"{key}_us"] = round(time_loop(torch, replay, n, warmup=3) * 1e6 / chains, 2)
+                out[f"{key}_submit_us"] = submit_us(replay, chains, n)
     return out
 
 
-def stage_report(torch, ch, reps, model):
+def stage_report(torch, device, ch, model, n=50):
+    """Each stage operator alone, `n` calls per graph (graph_time)."""
     out = {}
     for name in ch.stage_args:
-        sec = time_loop(torch, lambda: ch.stage(name), reps)
+        sec = graph_time(torch, device, lambda s: ch.stage(name, s), n=n)
         nbytes, flops = model[name]
         out[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "flops": flops,
                      "roofline": roofline(name, nbytes, flops, sec)}
     return out
 
 
-def launch_report(torch, ch, reps, model):
-    """Each launch of the fused chain alone (what chain_from_* runs)."""
+def launch_report(torch, device, ch, model, n=50):
+    """Each launch of the fused chain alone (what chain_from_* runs), `n`
+    launches per graph (graph_time)."""
     out = {}
     for index, name in enumerate(ch.rr.chain_fused_launch_names(ch.chain_args, ch.cfg.from_tokens)):
-        sec = time_loop(torch, lambda: ch.fused_launch(index), reps)
+        sec = graph_time(torch, device, lambda s: ch.fused_launch(index, s), n=n)
         nbytes, flops = model[name]
         out[name] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "flops": flops,
                      "roofline": roofline(name, nbytes, flops, sec)}
@@ -299,6 +433,11 @@ def launch_report(torch, ch, reps, model):
 # ------------------------------------------------------------------ workloads
 
 def headline(torch, device, args):
+    """The headline chain: `--warmup` untimed chains, then exactly `--steps`
+    chains in at most 20 batches (reference runner: each sample is the event
+    span of a batch divided by its size); value = T / p50 of the batch means.
+    Then the cold chain, the graph report and the per-launch / per-stage
+    breakdown (graph_time)."""
     from raggedroute_amd import workloads
     cfg = workloads.HEADLINE
     inputs = workloads.chain_inputs_device(cfg, 0, device)
@@ -306,39 +445,33 @@ def headline(torch, device, args):
     for _ in range(args.warmup):
         ch.chain()
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sizes = batch_sizes(args.steps)
     t0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        ch.chain()
-    stop.record()
+    means = batch_means(torch, ch.chain, sizes=sizes)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    elapsed = start.elapsed_time(stop) / 1e3
-    # per-chain p50 over single-chain event spans (reference runner p50 semantics)
-    spans = []
-    for _ in range(min(args.steps, 100)):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(); ch.chain(); b.record()
-        b.synchronize()
-        spans.append(a.elapsed_time(b) / 1e3)
-    warm = sample_stats(batch_means(torch, ch.chain, samples=20, repeats=10))
+    warm = sample_stats(means)
+    warm["batch_sizes"] = sorted(set(sizes))
+    mean_s = sum(m * n for m, n in zip(means, sizes)) / args.steps
     cold = sample_stats(cold_spans(torch, ch, device, samples=20))
     active = int((ch.counts.cpu().numpy() > 0).sum())
-    launches = launch_report(torch, ch, args.stage_reps,
+    launches = launch_report(torch, device, ch,
                              fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
-    ch.chain()  # restore y (timing launch 2 alone keeps adding into it)
+    ch.chain()  # restore y (timing the last launch alone keeps adding into it)
     graph = graph_report(torch, device, ch)
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
-    stages = stage_report(torch, ch, args.stage_reps, model)
-    return cfg, ch, inputs, {"elapsed_s": elapsed, "wall_s": wall, "p50_s": statistics.median(spans),
+    stages = stage_report(torch, device, ch, model)
+    return cfg, ch, inputs, {"p50_s": percentile(means, 0.5), "mean_s": mean_s, "wall_s": wall,
                              "warm": warm, "cold": cold, "graph": graph,
                              "launches": launches, "stages": stages, "active_experts": active}
 
 
-def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50, cpu_sample=False):
+def c4(torch, device, hidden=4096, output=14336, reps=5, samples=10, cpu_sample=False):
     """Mixtral-shaped ragged grouped GEMM + permute + unpermute: T=8192, R=16384,
-    E=8 with 7 active (Zipf 1.2), expert 7 empty."""
+    E=8 with 7 active (Zipf 1.2), expert 7 empty. Permute and unpermute are
+    timed warm (back-to-back calls: x, 134 MB, stays in the 256 MB Infinity
+    Cache) and cold (each call after a 512 MiB scrub); their roofline is the
+    cold one. The grouped GEMM (1.9 TFLOP, 1.9 GB of weights) is timed warm."""
     import raggedroute_amd as rr
     from raggedroute_amd import workloads
     t, e = 8192, 8
@@ -359,10 +492,18 @@ def c4(torch, device, hidden=4096, output=14336, reps=5, stage_reps=50, cpu_samp
     active = int((ch.counts.cpu().numpy() > 0).sum())
     model = work_model(t, e, hidden, output, active)
     out = {"T": t, "E": e, "K": hidden, "N": output, "active_experts": active}
-    for name, n_reps in (("token_permute", stage_reps), ("grouped_gemm", reps), ("unpermute", stage_reps)):
-        sec = time_loop(torch, lambda: ch.stage(name), n_reps, warmup=1)
+    for name in ("token_permute", "grouped_gemm", "unpermute"):
         nbytes, flops = model[name]
-        out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
+        if name == "grouped_gemm":
+            sec = time_loop(torch, lambda: ch.stage(name), reps, warmup=1)
+            out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
+            continue
+        warm = statistics.median(batch_means(torch, lambda: ch.stage(name), samples=samples, repeats=5))
+        cold = sample_stats(cold_spans(torch, ch, device, samples, call=lambda: ch.stage(name)))
+        cold_s = cold["p50_us"] * 1e-6
+        out[name] = {"us": cold["p50_us"], "cold": cold, "warm_us": round(warm * 1e6, 1),
+                     "warm_roofline": roofline(name, nbytes, flops, warm),
+                     "roofline": roofline(name, nbytes, flops, cold_s)}
     out["permute_gbs_reference_model"] = round(2 * 4 * 2 * t * hidden / (out["token_permute"]["us"] * 1e-6) / 1e9, 1)
     if cpu_sample:
         out["cpu_sample"] = cpu_sample_c4(ch, we, 2 * t)
@@ -378,10 +519,10 @@ def c5(torch, device, steps=20, cpu_sample=False):
     ch = Chain(cfg, inputs, device)
     sec = time_loop(torch, ch.chain, steps, warmup=3)
     active = int((ch.counts.cpu().numpy() > 0).sum())
-    launches = launch_report(torch, ch, 10,
-                             fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
+    launches = launch_report(torch, device, ch,
+                             fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active), n=5)
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
-    stages = stage_report(torch, ch, 10, model)
+    stages = stage_report(torch, device, ch, model, n=5)
     out = {"tokens_per_s": round(cfg.tokens / sec, 1), "chain_us": round(sec * 1e6, 1),
            "launches": launches, "stages": stages}
     if cpu_sample:
@@ -549,12 +690,23 @@ def trace_replay(torch, device, path=None, hidden=256, output=128, reps=100):
 
 
 def c3(torch, device):
+    """Fused histogram + exclusive scan at R = 2^20 (graph_time, warm and
+    cold), with its roofline, next to the launch floor: a trivial kernel
+    (a 64-byte cache scrub) timed alone and as three dependent launches."""
     import raggedroute_amd as rr
     from raggedroute_amd import workloads
     routes = 1 << 20
     out = {}
-    stream = torch.cuda.current_stream(device).cuda_stream
-    ctx = rr.RuntimeContext(stream=stream, architecture=int(rr.DeviceArchitecture.kGfx950))
+    tiny = torch.empty(16, dtype=torch.int32, device=device)
+
+    def trivial(stream, launches):
+        for _ in range(launches):
+            assert rr.ops.launch_cache_scrub(tiny.data_ptr(), 16, stream) == 0
+    one = graph_time(torch, device, lambda s: trivial(s, 1), n=50)
+    three = graph_time(torch, device, lambda s: trivial(s, 3), n=50)
+    out["launch_floor"] = {"one_trivial_kernel_us": round(one * 1e6, 2),
+                           "three_dependent_trivial_kernels_us": round(three * 1e6, 2)}
+    scrub = torch.empty(512 << 18, dtype=torch.int32, device=device)
     for experts in (1, 33, 256):
         for dist in ("uniform", "hot50"):
             ids = torch.from_numpy(workloads.route_ids(routes, experts, dist, 0)).to(device)
@@ -562,10 +714,26 @@ def c3(torch, device):
             offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
             args = rr.HistogramExclusiveScanArgs(expert_ids=ids.data_ptr(), counts=counts.data_ptr(),
                                                  offsets=offsets.data_ptr(), route_pairs=routes, experts=experts)
-            sec = time_loop(torch, lambda: rr.histogram_exclusive_scan(args, ctx), 50)
+
+            def call(stream):
+                ctx = rr.RuntimeContext(stream=stream, architecture=int(rr.DeviceArchitecture.kGfx950))
+                status = rr.histogram_exclusive_scan(args, ctx)
+                assert status.ok(), status.message
+            sec = graph_time(torch, device, call, n=50)
+            cold = []
+            cur = torch.cuda.current_stream(device).cuda_stream
+            for _ in range(10):
+                assert rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), cur) == 0
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(); call(cur); b.record()
+                b.synchronize()
+                cold.append(a.elapsed_time(b) / 1e3)
             nbytes = 4 * routes + 4 * experts + 4 * (experts + 1)
-            out[f"E{experts}_{dist}"] = {"us": round(sec * 1e6, 2),
-                                        "gbs": round(nbytes / sec / 1e9, 1)}
+            cold_s = statistics.median(cold)
+            out[f"E{experts}_{dist}"] = {"us": round(sec * 1e6, 2), "roofline": roofline("c3", nbytes, 0.0, sec),
+                                        "cold_us": round(cold_s * 1e6, 2),
+                                        "cold_roofline": roofline("c3", nbytes, 0.0, cold_s)}
+    del scrub
     return out
 
 
@@ -621,8 +789,157 @@ def profile(torch, device, case):
         torch.cuda.synchronize()
         print("profile: headline done (5 chains, 3 x each fused launch, 3 x each stage)", flush=True)
     elif case == "c4":
-        c4(torch, device, reps=2, stage_reps=2)
+        c4(torch, device, reps=2, samples=3)
         print("profile: c4 done", flush=True)
+    elif case == "c3":
+        c3(torch, device)
+        print("profile: c3 done", flush=True)
+
+
+# ------------------------------------------------------------ runner mode
+
+RUNNER_DEFAULTS = {"T": 4096, "E": 64, "K": 256, "N": 128, "top_k": 2, "distribution": "uniform",
+                   "zipf_s": None, "tie_fraction": 0.0, "seed": 0}
+
+
+def runner_params(pairs):
+    """--param key=value pairs over the defaults (the headline shape)."""
+    out = dict(RUNNER_DEFAULTS)
+    for pair in pairs:
+        key, sep, value = pair.partition("=")
+        if not sep or key not in out:
+            raise SystemExit(f"--param {pair!r}: expected key=value with key in {', '.join(out)}")
+        if key == "distribution":
+            out[key] = value
+        elif key in ("zipf_s", "tie_fraction"):
+            out[key] = float(value)
+        else:
+            out[key] = int(value)
+    return out
+
+
+def run_runner(torch, device, args):
+    """One chain entry or operator at any shape, timed with the reference
+    runner's semantics: `--warmup` calls, then `--samples` samples, each the
+    event span of `--kernel-repeats` back-to-back calls divided by the repeat
+    count (warm), or of one call after a `--cache-scrub-bytes` scrub
+    (cold_scrub); the reported value uses the p50 sample. Prints one JSON
+    record shaped like the headline line. Outputs are not validated here: the
+    tests check every entry against the oracle."""
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    p = runner_params(args.param)
+    t, e, k, n, top = p["T"], p["E"], p["K"], p["N"], p["top_k"]
+    family = {"auto": rr.KernelFamily.kAuto, "naive": rr.KernelFamily.kNaive,
+              "optimized": rr.KernelFamily.kOptimized}[args.variant]
+    kernel = rr.kernel(family, rr.GFX950_NATIVE if family == rr.KernelFamily.kOptimized else 0)
+    target = args.suite or args.operator
+    if target is None:
+        raise SystemExit("runner mode needs --suite or --operator")
+    stream = torch.cuda.current_stream(device).cuda_stream
+    keep = []  # device buffers the timed call reads or writes
+
+    if args.suite == "chain_from_route_ids":
+        cfg = workloads.RouteChainConfig("runner", t, e, k, n, top, p["distribution"],
+                                         p["zipf_s"] if p["zipf_s"] is not None else 1.4)
+        inp = workloads.route_chain_inputs(cfg, p["seed"])
+        d = {key: torch.from_numpy(np.ascontiguousarray(v)).to(device) for key, v in inp.items()}
+        r = t * top
+        i32 = dict(dtype=torch.int32, device=device)
+        bufs = {"counts": torch.empty(e, **i32), "offsets": torch.empty(e + 1, **i32),
+                "x_permuted": torch.empty(r, k, device=device), "route_pos": torch.empty(r, **i32),
+                "sorted_route": torch.empty(r, **i32), "y_permuted": torch.empty(r, n, device=device),
+                "y": torch.empty(t, n, device=device)}
+        rargs = rr.RouteChainArgs(
+            x=d["x"].data_ptr(), expert_ids=d["ids"].data_ptr(), route_weights=d["weights"].data_ptr(),
+            expert_weights=d["expert_weights"].data_ptr(), counts=bufs["counts"].data_ptr(),
+            offsets=bufs["offsets"].data_ptr(), x_permuted=bufs["x_permuted"].data_ptr(),
+            route_pos=bufs["route_pos"].data_ptr(), sorted_route=bufs["sorted_route"].data_ptr(),
+            y_permuted=bufs["y_permuted"].data_ptr(), y=bufs["y"].data_ptr(), tokens=t, experts=e,
+            top_k=top, hidden=k, output=n, kernel=kernel)
+        ws = torch.empty(max(1, rr.get_route_chain_workspace_size(rargs) // 4), **i32)
+        ctx = rr.RuntimeContext(stream=stream, workspace=ws.data_ptr(), workspace_bytes=ws.numel() * 4,
+                                architecture=int(rr.DeviceArchitecture.kGfx950))
+        keep += [d, bufs, ws]
+
+        def call():
+            status = rr.chain_from_route_ids(rargs, ctx)
+            if not status.ok():
+                raise RuntimeError(status.message)
+        unit_count, unit = t, "tokens/s"
+        nbytes = flops = None
+    else:
+        if top != 2:
+            raise SystemExit("chain_from_tokens / chain_from_logits and the operators run top_k = 2")
+        from_tokens = args.suite != "chain_from_logits" and args.operator != "topk_gate"
+        cfg = workloads.ChainConfig("runner", t, e, k, n, from_tokens=from_tokens,
+                                    logit_bias_s=p["zipf_s"], tie_fraction=p["tie_fraction"])
+        if from_tokens:
+            inputs = workloads.chain_inputs_device(cfg, p["seed"], device)
+        else:
+            inputs = {key: torch.from_numpy(v).to(device)
+                      for key, v in workloads.chain_inputs(cfg, p["seed"]).items() if key != "tie_rows"}
+        ch = Chain(cfg, inputs, device)
+        ch.chain_args.kernel = kernel
+        for _, op_args in ch.stage_args.values():
+            op_args.kernel = kernel
+        keep += [ch, inputs]
+        ch.chain()  # every intermediate an operator reads
+        if p["distribution"] != "uniform" and args.operator is not None:
+            ids = workloads.topk_route_ids(t, 2, e, p["distribution"], p["seed"],
+                                           p["zipf_s"] if p["zipf_s"] is not None else 1.4)
+            ch.ids.copy_(torch.from_numpy(ids.astype(np.int32)))
+            for name in ("histogram_scan", "token_permute", "grouped_gemm", "unpermute"):
+                ch.stage(name)
+        torch.cuda.synchronize()
+        active = int((ch.counts.cpu().numpy() > 0).sum())
+        if args.suite is not None:
+            call, unit_count, unit = ch.chain, t, "tokens/s"
+            nbytes = flops = None
+        else:
+            stage = {"histogram_exclusive_scan": "histogram_scan"}.get(args.operator, args.operator)
+            nbytes, flops = work_model(t, e, k, n, active)[stage]
+            call, unit_count, unit = (lambda: ch.stage(stage)), None, None
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    if args.profile_once:
+        call()
+        torch.cuda.synchronize()
+        return None
+    if args.cache_mode == "warm":
+        samples = batch_means(torch, call, samples=args.samples, repeats=args.kernel_repeats)
+        repeats = args.kernel_repeats
+    else:
+        scrub = torch.empty(max(1, args.cache_scrub_bytes // 4), dtype=torch.int32, device=device)
+        samples = []
+        for _ in range(args.samples):
+            assert rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), stream) == 0
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(); call(); b.record()
+            b.synchronize()
+            samples.append(a.elapsed_time(b) / 1e3)
+        repeats = 1
+        del scrub
+    p50 = percentile(samples, 0.5)
+    line = {"metric": f"{target} {'tokens/s' if unit else 'roofline rate'} @T{t}/E{e}/K{k}/N{n} FP32",
+            "n_gpus": 1, "steps": args.samples * repeats, "warmup": args.warmup,
+            "ms_per_step": round(p50 * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": f"synthetic (SplitMix64, seed {p['seed']})",
+            "config": {"workload": target, "T": t, "E": e, "K": k, "N": n, "top_k": top,
+                       "distribution": p["distribution"], "zipf_s": p["zipf_s"],
+                       "tie_fraction": p["tie_fraction"], "variant": args.variant,
+                       "cache_mode": args.cache_mode},
+            "samples": sample_stats(samples)}
+    if unit is not None:
+        line.update(value=round(unit_count / p50, 1), unit=unit)
+    else:
+        roof = roofline(target, nbytes, flops, p50)
+        line.update(value=roof["achieved"], unit=roof["unit"], roofline=roof,
+                    bytes=int(nbytes), flops=flops)
+    del keep
+    return line
 
 
 def main() -> int:
@@ -637,11 +954,16 @@ def main() -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.suite or args.operator:
+        line = run_runner(torch, device, args)
+        if line is not None:
+            print(json.dumps(line))
+        return 0
     if args.profile:
         profile(torch, device, args.profile)
         return 0
     cfg, ch, inputs, head = headline(torch, device, args)
-    tokens_per_s = cfg.tokens * args.steps / head["elapsed_s"]
+    tokens_per_s = cfg.tokens / head["p50_s"]
     launches = head["launches"]
     dominant = max(launches, key=lambda s: launches[s]["us"])
     roof = dict(launches[dominant]["roofline"])
@@ -709,8 +1031,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["elapsed_s"] / args.steps * 1e3, 4),
-        "p50_chain_us": round(head["p50_s"] * 1e6, 2),
+        "ms_per_step": round(head["p50_s"] * 1e3, 5),
+        "mean_chain_us": round(head["mean_s"] * 1e6, 2),
         "chain_warm": head["warm"],
         "chain_cold": head["cold"],
         "chain_graph": head["graph"],

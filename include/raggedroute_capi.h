@@ -395,12 +395,23 @@ typedef struct rr_chain_graph_cache_stats {
 
 rr_status rr_chain_graph_create(int32_t entry, const void* args, const rr_runtime_context* context,
                                 rr_chain_graph** graph);
+/* The same for `count` calls of one entry (args[i] each an rr_chain_args or
+ * rr_route_chain_args as `entry` says), recorded in order into one graph:
+ * e.g. the chains of every MoE layer of a model step, replayed with one
+ * hipGraphLaunch. 1 <= count <= 4096. One launch of a graph has a fixed cost
+ * on ROCm (about 19 us host, 5 us GPU on MI355X with ROCm 7.2): graphs of ten
+ * or more chains amortise it. */
+rr_status rr_chain_graph_create_sequence(int32_t entry, const void* const* args, int32_t count,
+                                         const rr_runtime_context* context, rr_chain_graph** graph);
 rr_status rr_chain_graph_launch(rr_chain_graph* graph, hipStream_t stream);
 /* Re-captures the graph's entry with new args (same entry) and updates the
  * executable in place (hipGraphExecUpdate); a changed launch plan is
  * instantiated anew. */
 rr_status rr_chain_graph_update(rr_chain_graph* graph, const void* args,
                                 const rr_runtime_context* context);
+/* Update of a sequence graph: the same entry and count as captured. */
+rr_status rr_chain_graph_update_sequence(rr_chain_graph* graph, const void* const* args, int32_t count,
+                                         const rr_runtime_context* context);
 int32_t rr_chain_graph_kernel_nodes(const rr_chain_graph* graph);
 void rr_chain_graph_destroy(rr_chain_graph* graph);
 /* Cache of executable graphs keyed by every pointer, size and kernel field of

@@ -158,16 +158,25 @@ def chain_fused_launch_names(args: ChainArgs, from_tokens: bool) -> list[str]:
 
 # ---- chain graphs (rr_chain_graph_*, rr_chain_graph_cache_*) ----
 
+def _arg_pointers(args):
+    return (ctypes.c_void_p * len(args))(*[ctypes.addressof(a) for a in args])
+
+
 class ChainGraph:
-    """One chain call captured into an executable HIP graph. `entry` is
+    """Chain calls captured into one executable HIP graph. `entry` is
     CHAIN_FROM_TOKENS / CHAIN_FROM_LOGITS (ChainArgs) or CHAIN_FROM_ROUTE_IDS
-    (RouteChainArgs); raises RuntimeError with the library's message when the
-    call cannot be captured."""
+    (RouteChainArgs); `args` is one args struct or a list of them (recorded
+    in order, replayed by one launch). Raises RuntimeError with the library's
+    message when the calls cannot be captured."""
 
     def __init__(self, entry: int, args, context: RuntimeContext):
         self._handle = ctypes.c_void_p()
         self.entry = entry
-        st = lib.rr_chain_graph_create(entry, ctypes.addressof(args), byref(context), byref(self._handle))
+        if isinstance(args, (list, tuple)):
+            ptrs = _arg_pointers(args)
+            st = lib.rr_chain_graph_create_sequence(entry, ptrs, len(args), byref(context), byref(self._handle))
+        else:
+            st = lib.rr_chain_graph_create(entry, ctypes.addressof(args), byref(context), byref(self._handle))
         if not st.ok():
             raise RuntimeError(st.message)
 
@@ -175,6 +184,8 @@ class ChainGraph:
         return lib.rr_chain_graph_launch(self._handle, stream)
 
     def update(self, args, context: RuntimeContext) -> Status:
+        if isinstance(args, (list, tuple)):
+            return lib.rr_chain_graph_update_sequence(self._handle, _arg_pointers(args), len(args), byref(context))
         return lib.rr_chain_graph_update(self._handle, ctypes.addressof(args), byref(context))
 
     @property

@@ -352,6 +352,9 @@ PROTOTYPES += [
     ("rr_chain_graph_create", Status, [c_int32, c_void_p, POINTER(RuntimeContext), POINTER(c_void_p)]),
     ("rr_chain_graph_launch", Status, [c_void_p, c_void_p]),
     ("rr_chain_graph_update", Status, [c_void_p, c_void_p, POINTER(RuntimeContext)]),
+    ("rr_chain_graph_create_sequence", Status,
+     [c_int32, POINTER(c_void_p), c_int32, POINTER(RuntimeContext), POINTER(c_void_p)]),
+    ("rr_chain_graph_update_sequence", Status, [c_void_p, POINTER(c_void_p), c_int32, POINTER(RuntimeContext)]),
     ("rr_chain_graph_kernel_nodes", c_int32, [c_void_p]),
     ("rr_chain_graph_destroy", None, [c_void_p]),
     ("rr_chain_graph_cache_create", Status, [c_int32, POINTER(c_void_p)]),

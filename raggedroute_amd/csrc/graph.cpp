@@ -1,5 +1,6 @@
-// Chain graphs: one chain call captured into an executable HIP graph, replayed
-// with a single hipGraphLaunch (the reference's CUDA-graph chain variants,
+// Chain graphs: one chain call, or a sequence of chain calls (one per MoE
+// layer of a model step, say), captured into an executable HIP graph and
+// replayed with a single hipGraphLaunch (the reference's CUDA-graph chain variants,
 // benchmarks/adapters/chain_adapter.cpp:730-826 fixed capture / exec update,
 // :962-1000 shape cache; postroute_chain_adapter.cpp the same for the
 // post-route chain).
@@ -9,6 +10,12 @@
 // nodes are kept out of graphs. A graph bakes every kernel argument (pointers,
 // sizes) at capture; the device buffers must outlive it, and their contents
 // are read at replay time. Graph and cache objects are not thread-safe.
+//
+// On ROCm 7.2 one hipGraphLaunch has a fixed cost (measured on MI355X: about
+// 19 us of host time and 5 us of GPU time before the first node) that a graph
+// of one headline chain (two kernels, ~23 us) does not win back; a sequence
+// of ten or more chains per graph runs at the direct calls' GPU time with a
+// fraction of their host submission time.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -22,6 +29,7 @@ struct rr_chain_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int32_t entry = 0;
+  int32_t calls = 1;  // chain calls recorded, in order
   int32_t kernel_nodes = 0;
 };
 
@@ -63,13 +71,17 @@ rr_status run_entry(int32_t entry, const void* args, const rr_runtime_context* c
   }
 }
 
-// Records one call on context->stream (thread-local capture) into *graph.
-rr_status capture(int32_t entry, const void* args, const rr_runtime_context* context,
-                  hipGraph_t* graph) noexcept {
+// Records `count` calls of one entry, in order, on context->stream
+// (thread-local capture) into *graph.
+rr_status capture(int32_t entry, const void* const* args, int32_t count,
+                  const rr_runtime_context* context, hipGraph_t* graph) noexcept {
   *graph = nullptr;
   hipError_t err = hipStreamBeginCapture(context->stream, hipStreamCaptureModeThreadLocal);
   if (err != hipSuccess) return device_status(err, "chain graph capture could not begin");
-  const rr_status status = run_entry(entry, args, context);
+  rr_status status = ok_status();
+  for (int32_t i = 0; i < count && status.code == RR_STATUS_SUCCESS; ++i) {
+    status = run_entry(entry, args[i], context);
+  }
   hipGraph_t captured = nullptr;
   err = hipStreamEndCapture(context->stream, &captured);
   if (status.code != RR_STATUS_SUCCESS) {
@@ -81,6 +93,18 @@ rr_status capture(int32_t entry, const void* args, const rr_runtime_context* con
     return device_status(err, "chain graph capture failed");
   }
   *graph = captured;
+  return ok_status();
+}
+
+rr_status check_calls(int32_t entry, const void* const* args, int32_t count,
+                      const rr_runtime_context* context) noexcept {
+  if (args == nullptr || count < 1 || count > 4096) {
+    return invalid_argument("chain graph needs 1 to 4096 calls and their args");
+  }
+  for (int32_t i = 0; i < count; ++i) {
+    const rr_status status = check_call(entry, args[i], context);
+    if (status.code != RR_STATUS_SUCCESS) return status;
+  }
   return ok_status();
 }
 
@@ -118,16 +142,17 @@ void release(rr_chain_graph* g) noexcept {
   g->graph = nullptr;
 }
 
-rr_status create(int32_t entry, const void* args, const rr_runtime_context* context,
-                 rr_chain_graph** out) noexcept {
+rr_status create(int32_t entry, const void* const* args, int32_t count,
+                 const rr_runtime_context* context, rr_chain_graph** out) noexcept {
   if (out == nullptr) return invalid_argument("chain graph output handle must not be null");
   *out = nullptr;
-  rr_status status = check_call(entry, args, context);
+  rr_status status = check_calls(entry, args, count, context);
   if (status.code != RR_STATUS_SUCCESS) return status;
   auto* g = new (std::nothrow) rr_chain_graph;
   if (g == nullptr) return make_status(RR_STATUS_DEVICE_ERROR, "chain graph allocation failed");
   g->entry = entry;
-  status = capture(entry, args, context, &g->graph);
+  g->calls = count;
+  status = capture(entry, args, count, context, &g->graph);
   if (status.code == RR_STATUS_SUCCESS) status = instantiate(g, context->stream);
   if (status.code != RR_STATUS_SUCCESS) {
     release(g);
@@ -139,14 +164,17 @@ rr_status create(int32_t entry, const void* args, const rr_runtime_context* cont
   return ok_status();
 }
 
-// New arguments for an existing graph: capture them and update the
-// executable in place when the topology matches, else instantiate anew.
-rr_status update(rr_chain_graph* g, const void* args, const rr_runtime_context* context) noexcept {
+// New arguments for an existing graph (same entry, same number of calls):
+// capture them and update the executable in place when the topology
+// matches, else instantiate anew.
+rr_status update(rr_chain_graph* g, const void* const* args, int32_t count,
+                 const rr_runtime_context* context) noexcept {
   if (g == nullptr) return invalid_argument("chain graph must not be null");
-  rr_status status = check_call(g->entry, args, context);
+  if (count != g->calls) return invalid_argument("chain graph update needs as many calls as were captured");
+  rr_status status = check_calls(g->entry, args, count, context);
   if (status.code != RR_STATUS_SUCCESS) return status;
   hipGraph_t fresh = nullptr;
-  status = capture(g->entry, args, context, &fresh);
+  status = capture(g->entry, args, count, context, &fresh);
   if (status.code != RR_STATUS_SUCCESS) return status;
   hipGraphNode_t error_node = nullptr;
   hipGraphExecUpdateResult result = hipGraphExecUpdateError;
@@ -226,7 +254,12 @@ extern "C" {
 
 rr_status rr_chain_graph_create(int32_t entry, const void* args, const rr_runtime_context* context,
                                 rr_chain_graph** graph) {
-  return rr::create(entry, args, context, graph);
+  return rr::create(entry, &args, 1, context, graph);
+}
+
+rr_status rr_chain_graph_create_sequence(int32_t entry, const void* const* args, int32_t count,
+                                         const rr_runtime_context* context, rr_chain_graph** graph) {
+  return rr::create(entry, args, count, context, graph);
 }
 
 rr_status rr_chain_graph_launch(rr_chain_graph* graph, hipStream_t stream) {
@@ -236,7 +269,12 @@ rr_status rr_chain_graph_launch(rr_chain_graph* graph, hipStream_t stream) {
 
 rr_status rr_chain_graph_update(rr_chain_graph* graph, const void* args,
                                 const rr_runtime_context* context) {
-  return rr::update(graph, args, context);
+  return rr::update(graph, &args, 1, context);
+}
+
+rr_status rr_chain_graph_update_sequence(rr_chain_graph* graph, const void* const* args, int32_t count,
+                                         const rr_runtime_context* context) {
+  return rr::update(graph, args, count, context);
 }
 
 int32_t rr_chain_graph_kernel_nodes(const rr_chain_graph* graph) {
@@ -279,7 +317,7 @@ rr_status rr_chain_graph_cache_launch(rr_chain_graph_cache* cache, int32_t entry
     }
   }
   rr_chain_graph* g = nullptr;
-  status = rr::create(entry, args, context, &g);
+  status = rr::create(entry, &args, 1, context, &g);
   if (status.code != RR_STATUS_SUCCESS) return status;
   ++cache->misses;
   try {

@@ -542,6 +542,7 @@ __global__ __launch_bounds__(WAVES * 64) void rr_route_prep_kernel(
 // is not a multiple of 4 element by element. Rows of any width and offset
 // stay on vector loads and stores.
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef int i4u __attribute__((ext_vector_type(4), aligned(4)));
 
 __host__ __device__ inline uint32_t quads_of(int width) { return (static_cast<uint32_t>(width) + 3u) / 4u; }
 
@@ -631,9 +632,13 @@ __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restri
 // lane j reads route j's position once per row (routes beyond the first 64 of
 // a row, possible only in the stand-alone permute, are read 64 at a time),
 // then the lanes stride over the row's quads, eight in flight per lane (x read
-// once, written top_k times). Output rows go out with nontemporal stores: they
-// are not read again by the kernel, and streaming them past the caches cut
-// the C4 copy (T = 8192, 16 KB rows) from 89 to 69 us.
+// once, written top_k times). Rows are read and written with nontemporal
+// accesses, four blocks per CU. Measured at C4 (T = 8192, 16 KB rows, 403 MB):
+// with cached loads the copy took 61 us while x sat in the Infinity Cache but
+// 106-111 us cold (after a read-modify-write scrub the cache holds dirty
+// lines, and every allocating load evicts one: extra write-back traffic), for
+// any grid of 256-2048 blocks and 4-16 quads in flight; nontemporal loads take
+// 79-82 us warm and cold alike (5.0 TB/s). Nontemporal stores: 89 -> 69 us.
 constexpr int kRowQuadsInFlight = 8;
 
 __global__ __launch_bounds__(256) void rr_permute_rows_kernel(const float* __restrict__ x,
@@ -655,7 +660,7 @@ __global__ __launch_bounds__(256) void rr_permute_rows_kernel(const float* __res
       for (int u = 0; u < kRowQuadsInFlight; ++u) {
         const int k0 = 4 * (q0 + lane + 64 * u);
         if (k0 + 4 <= hidden) {
-          v[u] = *reinterpret_cast<const f4u*>(src + k0);
+          v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(src + k0));
         } else {
           v[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
           for (int e = 0; k0 + e < hidden; ++e) v[u][e] = src[k0 + e];
@@ -676,6 +681,182 @@ __global__ __launch_bounds__(256) void rr_permute_rows_kernel(const float* __res
             } else {
               for (int e = 0; k0 + e < hidden; ++e) dst[k0 + e] = v[u][e];
             }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Wide rows (hidden >= 1024) with few routes: the stable rank and the row
+// copy in one launch. Block b owns tokens [b * tpb, (b + 1) * tpb), so routes
+// [b * tpb * top_k, ...). Each wave first issues the nontemporal loads of its
+// first row's first quads; then the block recounts every earlier route per
+// expert and ranks its own routes (as rr_permute_rank_kernel does), keeping
+// their positions in LDS besides route_pos / sorted_route; then the waves copy
+// their tokens' rows. The rank phase runs under the first loads' latency and
+// the copy waits for no second launch. The recount reads the routes before a
+// block's range, so the host keeps this kernel to R <= kFusedRankRoutes.
+constexpr int kFusedRankRoutes = 32768;
+constexpr int kFusedWaves = 4;
+
+__global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
+    const float* __restrict__ x, const int32_t* __restrict__ ids, const int32_t* __restrict__ offsets,
+    int32_t* cursors, float* __restrict__ x_permuted, int32_t* __restrict__ route_pos,
+    int32_t* __restrict__ sorted_route, int tokens, int top_k, int hidden, int experts, int bits,
+    int tokens_per_block) {
+  constexpr int kThreads = kFusedWaves * 64;
+  extern __shared__ int32_t lds[];
+  int32_t* wc = lds;                           // [waves][experts]
+  int32_t* base = lds + kFusedWaves * experts;  // [experts]
+  int32_t* slot = base + experts;               // [tokens_per_block * top_k] my routes' positions
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int routes = tokens * top_k;
+  const int t_begin = static_cast<int>(blockIdx.x) * tokens_per_block;
+  const int t_end = t_begin + tokens_per_block < tokens ? t_begin + tokens_per_block : tokens;
+  const int begin = t_begin * top_k;
+  const int end = t_end * top_k;
+  const int cols = static_cast<int>(quads_of(hidden));
+
+  f4u v[kRowQuadsInFlight];
+  auto load_chunk = [&](const float* src, int q0) {
+#pragma unroll
+    for (int u = 0; u < kRowQuadsInFlight; ++u) {
+      const int k0 = 4 * (q0 + lane + 64 * u);
+      if (k0 + 4 <= hidden) {
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(src + k0));
+      } else {
+        v[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
+        for (int e = 0; k0 + e < hidden; ++e) v[u][e] = src[k0 + e];
+      }
+    }
+  };
+  // The first row's first chunk stays in flight while the block ranks.
+  const int t_first = t_begin + wave;
+  constexpr int kChunk = 64 * kRowQuadsInFlight;  // quads per chunk
+  if (t_first < t_end) load_chunk(x + static_cast<std::size_t>(t_first) * hidden, 0);
+
+  // ---- rank phase (block-wide) ----
+  for (int i = tid; i < kFusedWaves * experts; i += kThreads) wc[i] = 0;
+  __syncthreads();
+  // Count the shorter side of the block's first route: the routes before it,
+  // or (past the middle) the routes from it on, whose per-expert counts are
+  // subtracted from the expert's total offsets[e + 1] - offsets[e] below.
+  const bool suffix = begin > routes - begin;
+  const int c_lo = suffix ? begin : 0;
+  const int c_hi = suffix ? routes : begin;
+  {
+    // 16-byte id loads, eight per lane in flight. E <= 16: per-lane packed
+    // 8-bit counters (expert e in bits 8 (e % 8) of word e / 8; a lane counts
+    // at most R / 256 <= 128 ids here), summed over the wave afterwards;
+    // else one LDS atomic per id into the wave's row.
+    constexpr int kBatch = 8;
+    const bool few = experts <= 16;
+    uint64_t packed[2] = {0, 0};
+    for (int b0 = c_lo; b0 < c_hi; b0 += 4 * kThreads * kBatch) {
+      i4u id[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int r = b0 + 4 * (tid + kThreads * u);
+        if (r + 4 <= c_hi) {
+          id[u] = *reinterpret_cast<const i4u*>(ids + r);
+        } else {
+          id[u] = i4u{-1, -1, -1, -1};
+          for (int c = 0; r + c < c_hi; ++c) id[u][c] = ids[r + c];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int v = id[u][c];
+          if (static_cast<unsigned>(v) >= static_cast<unsigned>(experts)) continue;
+          if (few) {
+            const uint64_t one = uint64_t{1} << (8 * (v & 7));
+            packed[0] += v < 8 ? one : 0;
+            packed[1] += v < 8 ? 0 : one;
+          } else {
+            atomicAdd(wc + wave * experts + v, 1);
+          }
+        }
+      }
+    }
+    if (few) {
+      for (int e = 0; e < experts; ++e) {
+        const int32_t n = static_cast<int32_t>((packed[e >> 3] >> (8 * (e & 7))) & 0xff);
+        const int32_t total = __builtin_amdgcn_readlane(wave_inclusive_scan(n), 63);
+        if (lane == 0) wc[wave * experts + e] = total;
+      }
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < experts; e += kThreads) {
+    int32_t sum = 0;
+    for (int w = 0; w < kFusedWaves; ++w) {
+      sum += wc[w * experts + e];
+      wc[w * experts + e] = 0;
+    }
+    base[e] = suffix ? offsets[e + 1] - offsets[e] - sum : sum;
+  }
+  __syncthreads();
+  for (int sub = begin; sub < end; sub += kThreads) {
+    const int r = sub + tid;
+    const int id = r < end ? ids[r] : -1;
+    const bool valid = id >= 0 && id < experts;
+    const uint64_t active = __ballot(valid);
+    const uint64_t mask = match_mask(static_cast<uint32_t>(valid ? id : 0), bits, active);
+    const int rank = __popcll(mask & lanemask_lt());
+    const bool leader = valid && rank == 0;
+    if (leader) wc[wave * experts + id] = __popcll(mask);
+    __syncthreads();
+    for (int e = tid; e < experts; e += kThreads) {
+      int32_t running = base[e];
+      for (int w = 0; w < kFusedWaves; ++w) {
+        const int32_t c = wc[w * experts + e];
+        if (c != 0) {
+          wc[w * experts + e] = running;
+          running += c;
+        }
+      }
+      base[e] = running;
+    }
+    __syncthreads();
+    if (r < end) {
+      int32_t pos = -1;
+      if (valid) {
+        pos = offsets[id] + wc[wave * experts + id] + rank;
+        if (pos < 0 || pos >= routes) pos = -1;  // offsets inconsistent with ids
+      }
+      route_pos[r] = pos;
+      slot[r - begin] = pos;
+      if (sorted_route != nullptr && pos >= 0) sorted_route[pos] = r;
+    }
+    if (leader) wc[wave * experts + id] = 0;  // (as in rr_permute_rank_kernel)
+    __syncthreads();  // slot entries and cleared rows before the next sub-chunk / the copy
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    for (int e = tid; e < experts; e += kThreads) cursors[e] = base[e];
+  }
+
+  // ---- copy phase: wave w copies rows t_begin + w, + waves, ... ----
+  for (int t = t_first; t < t_end; t += kFusedWaves) {
+    const float* src = x + static_cast<std::size_t>(t) * hidden;
+    const int32_t* my_slots = slot + (t - t_begin) * top_k;
+    for (int q0 = 0; q0 < cols; q0 += kChunk) {
+      if (t != t_first || q0 != 0) load_chunk(src, q0);
+      for (int j = 0; j < top_k; ++j) {
+        const int32_t pos = my_slots[j];  // (one LDS address: a broadcast)
+        if (pos < 0) continue;            // wave-uniform
+        float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden;
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) {
+          const int k0 = 4 * (q0 + lane + 64 * u);
+          if (k0 + 4 <= hidden) {
+            __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(dst + k0));
+          } else {
+            for (int e = 0; k0 + e < hidden; ++e) dst[k0 + e] = v[u][e];
           }
         }
       }
@@ -789,12 +970,19 @@ unsigned row_grid(int rows) {
   return static_cast<unsigned>(blocks < 256 ? (blocks == 0 ? 1 : blocks) : 256);
 }
 
+unsigned copy_row_grid(int rows) {
+  // One wave per row, four waves per block, four blocks per CU (the copy's
+  // nontemporal loads want more rows in flight than the unpermute's).
+  const int blocks = (rows + 3) / 4;
+  return static_cast<unsigned>(blocks < 1024 ? (blocks == 0 ? 1 : blocks) : 1024);
+}
+
 hipError_t launch_permute_copy(const float* x, const int32_t* route_pos, float* x_permuted,
                                int tokens, int top_k, int hidden, int routes, hipStream_t stream) {
   if (hidden >= kWideRow) {
     if (hidden > kMaxRowWidth) return hipErrorInvalidValue;
-    rr_permute_rows_kernel<<<row_grid(tokens), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
-                                                                 top_k, hidden, routes);
+    rr_permute_rows_kernel<<<copy_row_grid(tokens), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
+                                                                      top_k, hidden, routes);
   } else {
     const uint64_t items = static_cast<uint64_t>(tokens) * quads_of(hidden);
     if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;  // 32-bit item indices
@@ -864,6 +1052,19 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
                                 int hidden, hipStream_t stream) {
   const int routes = tokens * top_k;
   if (routes <= 0) return hipSuccess;
+  if (hidden >= kWideRow && hidden <= kMaxRowWidth && routes <= kFusedRankRoutes) {
+    // rank + copy in one launch: up to four blocks per CU, whole tokens each
+    const int grid = tokens < 1024 ? tokens : 1024;
+    const int tpb = (tokens + grid - 1) / grid;
+    const int blocks = (tokens + tpb - 1) / tpb;
+    const std::size_t lds =
+        (static_cast<std::size_t>(kFusedWaves + 1) * experts + static_cast<std::size_t>(tpb) * top_k) *
+        sizeof(int32_t);
+    rr_permute_rank_rows_kernel<<<blocks, kFusedWaves * 64, lds, stream>>>(
+        x, ids, offsets, cursors, x_permuted, route_pos, sorted_route, tokens, top_k, hidden, experts,
+        bits_for(experts), tpb);
+    return hipGetLastError();
+  }
   // One sub-chunk per block up to 64 blocks; beyond that the chunk grows so the
   // recomputed prefix stays bounded by 64 chunks. 16 waves while (16 + 1) LDS
   // rows of E ints fit in 34 KB, else 8 waves.

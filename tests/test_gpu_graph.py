@@ -203,3 +203,41 @@ def test_graph_rejections(device):
         rr.ChainGraph(rr.CHAIN_FROM_LOGITS, run.args, _side_ctx(run, stream))
     with pytest.raises(RuntimeError):
         rr.ChainGraphCache(0)
+
+
+def test_graph_sequence_of_chains(device):
+    """Three chain calls with their own buffers and shapes (three MoE layers
+    of a step) recorded into one graph: every replay writes each layer's
+    outputs bit-identically to that layer's eager call; an update with the
+    layers' args in another order rebinds them; an update with another call
+    count is rejected."""
+    cfgs = [workloads.HEADLINE, workloads.C1, workloads.ChainConfig("seq3", 700, 16, 300, 40)]
+    inps = [workloads.chain_inputs(c, seed=40 + i) for i, c in enumerate(cfgs)]
+    eager = [ChainRun(c, x, device) for c, x in zip(cfgs, inps)]
+    graphed = [ChainRun(c, x, device) for c, x in zip(cfgs, inps)]
+    stream = torch.cuda.Stream(device)
+    # one workspace large enough for every layer (calls run in order)
+    ws = max(graphed, key=lambda r: r.ws.numel()).ws
+    ctx = rr.RuntimeContext(stream=stream.cuda_stream, workspace=ws.data_ptr(), workspace_bytes=ws.numel() * 4,
+                            architecture=int(rr.DeviceArchitecture.kGfx950))
+    for run in eager:
+        run.run(_side_ctx(run, stream))
+    with rr.ChainGraph(rr.CHAIN_FROM_TOKENS, [g.args for g in graphed], ctx) as graph:
+        assert graph.kernel_nodes >= 6
+        for order in ([0, 1, 2], [2, 0, 1]):
+            if order != [0, 1, 2]:
+                st = graph.update([graphed[i].args for i in order], ctx)
+                assert st.ok(), st.message
+            for _ in range(3):
+                for run in graphed:
+                    _poison(run, CHAIN_OUT)
+                eager[1].run(_side_ctx(eager[1], stream))  # eager work between replays
+                torch.cuda.synchronize()
+                st = graph.launch(stream.cuda_stream)
+                assert st.ok(), st.message
+                torch.cuda.synchronize()
+                for e, g in zip(eager, graphed):
+                    for name in CHAIN_OUT:
+                        assert _same(getattr(g, name), getattr(e, name)), f"{g.cfg.name}: {name} differs"
+        st = graph.update([graphed[0].args, graphed[1].args], ctx)
+        assert st.code == rr.StatusCode.kInvalidArgument

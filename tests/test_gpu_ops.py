@@ -352,6 +352,11 @@ def test_permute_unaligned_duplicate_ids(ctx, device, kat, kernel):
     # pass of a wave (2048 floats) with a 3-float tail, more than 64 routes per
     # token (position lanes read in chunks of 64); item kernel with many routes
     (50, 8, 2, 2051), (20, 200, 100, 1500), (9, 16, 3, 1024), (40, 200, 130, 9), (17, 1024, 1024, 5),
+    # wide rows, rank + copy in one launch: several tokens per block and wave,
+    # top_k 4 with a 7-float tail; beyond 32768 routes the two-launch path
+    (2500, 64, 2, 1100), (1500, 300, 4, 1031), (17000, 8, 2, 1024),
+    # ... few experts (ballot recount) with block prefixes that end mid-quad
+    (3001, 16, 3, 1030), (4100, 5, 1, 1024),
 ])
 def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     rng = np.random.default_rng(tokens + experts)

@@ -307,3 +307,33 @@ def test_cpp_consumer_compiles_links_and_runs(tmp_path):
     assert build.returncode == 0, build.stderr
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert run.returncode == 0 and "consumer OK" in run.stdout, run.stdout + run.stderr
+
+
+def test_chain_graph_argument_checks_before_capture():
+    """Graph entries reject bad calls before any device work: a null handle
+    slot, no args, a call count outside [1, 4096], an unknown entry, the
+    default stream and the naive family (memset resets stay out of graphs)."""
+    import ctypes
+    handle = ctypes.c_void_p()
+    ctx = rr.RuntimeContext(stream=0x1234, architecture=GFX950)
+    args = rr.ChainArgs(tokens=4, experts=4, hidden=8, output=8)
+    one = (ctypes.c_void_p * 1)(ctypes.addressof(args))
+    bad = [
+        rr.lib.rr_chain_graph_create_sequence(rr.CHAIN_FROM_TOKENS, one, 0, ctypes.byref(ctx), ctypes.byref(handle)),
+        rr.lib.rr_chain_graph_create_sequence(rr.CHAIN_FROM_TOKENS, None, 1, ctypes.byref(ctx), ctypes.byref(handle)),
+        rr.lib.rr_chain_graph_create_sequence(rr.CHAIN_FROM_TOKENS, one, 4097, ctypes.byref(ctx), ctypes.byref(handle)),
+        rr.lib.rr_chain_graph_create_sequence(7, one, 1, ctypes.byref(ctx), ctypes.byref(handle)),
+        rr.lib.rr_chain_graph_create_sequence(rr.CHAIN_FROM_TOKENS, one, 1,
+                                              ctypes.byref(rr.RuntimeContext(architecture=GFX950)),
+                                              ctypes.byref(handle)),
+        rr.lib.rr_chain_graph_create_sequence(rr.CHAIN_FROM_TOKENS, one, 1, ctypes.byref(ctx), None),
+    ]
+    naive = rr.ChainArgs(tokens=4, experts=4, hidden=8, output=8, kernel=rr.kernel(rr.KernelFamily.kNaive))
+    bad.append(rr.lib.rr_chain_graph_create_sequence(
+        rr.CHAIN_FROM_TOKENS, (ctypes.c_void_p * 1)(ctypes.addressof(naive)), 1, ctypes.byref(ctx),
+        ctypes.byref(handle)))
+    for st in bad:
+        assert st.code == rr.StatusCode.kInvalidArgument, st
+    assert not handle.value
+    st = rr.lib.rr_chain_graph_update_sequence(None, one, 1, ctypes.byref(ctx))
+    assert st.code == rr.StatusCode.kInvalidArgument
