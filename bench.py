@@ -58,7 +58,7 @@ def parse(argv=None):
     ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
     ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route,trace")
     ap.add_argument("--route-trace", default="", help="replay every frame of this .rrtrace file (extras.route_trace)")
-    ap.add_argument("--profile", default="", choices=["", "headline", "c4", "c3"],
+    ap.add_argument("--profile", default="", choices=["", "headline", "c4", "c3", "c5"],
                     help="profiler driver: a fixed number of launches of one case, no timing, "
                          "no JSON line (for rocprofv3 --pmc / --kernel-trace runs)")
     # shape-generic runner (reference benchmarks/benchmark_main.cpp:16-33)
@@ -794,6 +794,16 @@ def profile(torch, device, case):
     elif case == "c3":
         c3(torch, device)
         print("profile: c3 done", flush=True)
+    elif case == "c5":
+        cfg = workloads.C5
+        ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
+        for _ in range(3):
+            ch.chain()
+        for name in ("grouped_gemm",):
+            for _ in range(3):
+                ch.stage(name)
+        torch.cuda.synchronize()
+        print("profile: c5 done (3 chains, 3 x grouped_gemm)", flush=True)
 
 
 # ------------------------------------------------------------ runner mode

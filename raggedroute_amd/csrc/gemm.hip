@@ -235,14 +235,35 @@ __device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles,
   *ct = within / rows_in_group;
 }
 
+// Wave layouts of a tile's MFMA work. WaveLayout: the tile shape's WM x WN
+// grid of (BM / WM) x (BN / WN) wave tiles. SlabLayout: every wave takes all
+// TM 16-row blocks of the tile's top rows and a COLS-wide column slab.
+template <int TM_, int TN_, class S>
+struct WaveLayout {
+  static constexpr int kTM = TM_;
+  static constexpr int kTN = TN_;
+  __device__ static int wm0(int wave) { return (wave / S::WN) * (S::BM / S::WM); }
+  __device__ static int wn0(int wave) { return (wave % S::WN) * (S::BN / S::WN); }
+};
+template <int TM_, int TN_, int COLS>
+struct SlabLayout {
+  static constexpr int kTM = TM_;
+  static constexpr int kTN = TN_;
+  __device__ static int wm0(int) { return 0; }
+  __device__ static int wn0(int wave) { return wave * COLS; }
+};
+
 template <class S, bool VEC, int MODE>
 __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams prm) {
   constexpr bool kGroupedRows = MODE == kGrouped || MODE == kChainGrouped;
+  // slab layouts for tiles of at most 64 rows (the 128 x 128 tile, 2 x 2 waves)
+  constexpr bool kSlabs = S::BM == 128 && S::BN == 128 && S::WM == 2 && S::WN == 2;
   extern __shared__ float lds[];
   float* stages = lds;                                                              // kStages
   int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * S::kStageFloats);  // [E + 1]
-  int32_t* s_pre = s_off + prm.experts + 1;                                          // [E + 1]
-  int32_t* s_src = s_pre + prm.experts + 1;  // [BM] chain: token row of X per tile row
+  int32_t* s_pre = s_off + prm.experts + 1;   // [E + 1] full row tiles before expert e
+  int32_t* s_pre2 = s_pre + prm.experts + 1;  // [E + 1] short row tiles before expert e
+  int32_t* s_src = s_pre2 + prm.experts + 1;  // [BM] chain: token row of X per tile row
   float* s_w = reinterpret_cast<float*>(s_src + S::BM);  // [BM] chain: route weight per tile row
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = rr::dev::lane_id();
@@ -251,38 +272,61 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
   const int K = prm.K;
   const int N = prm.N;
 
-  // ---- device-side scheduler: per-expert row-tile prefix in LDS ----
+  // ---- device-side scheduler: per-expert row-tile prefixes in LDS ----
+  // With slab layouts (below) an expert's last row tile is "short" when it
+  // holds at most BM / 2 rows: its MFMA work is a fraction of a full tile's.
+  // The tile space lists every full tile first and the short ones after, so
+  // the grid-stride rounds finish on cheap tiles instead of putting a short
+  // tile's worker behind a full round.
   for (int e = tid; e <= experts; e += S::kThreads) {
     s_off[e] = kGroupedRows ? prm.offsets[e] : (e == 0 ? 0 : prm.dense_rows);
   }
   __syncthreads();
+  auto full_tiles = [](int32_t cnt) -> int32_t {
+    if (cnt <= 0) return 0;
+    if constexpr (kSlabs) return cnt / S::BM + (cnt % S::BM > S::BM / 2 ? 1 : 0);
+    return (cnt + S::BM - 1) / S::BM;
+  };
+  auto short_tiles = [](int32_t cnt) -> int32_t {
+    if constexpr (kSlabs) return cnt > 0 && cnt % S::BM != 0 && cnt % S::BM <= S::BM / 2 ? 1 : 0;
+    return 0;
+  };
   if (wave == 0) {
     // Lane l owns experts [l*per, (l+1)*per); experts <= 1024 -> per <= 16.
     const int per = (experts + 63) / 64;
-    int32_t local = 0;
+    int32_t local = 0, local2 = 0;
     for (int j = 0; j < per; ++j) {
       const int e = lane * per + j;
       if (e < experts) {
         const int32_t cnt = s_off[e + 1] - s_off[e];
-        local += cnt > 0 ? (cnt + S::BM - 1) / S::BM : 0;
+        local += full_tiles(cnt);
+        local2 += short_tiles(cnt);
       }
     }
     const int32_t incl = rr::dev::wave_inclusive_scan(local);
-    int32_t run = incl - local;
+    const int32_t incl2 = rr::dev::wave_inclusive_scan(local2);
+    int32_t run = incl - local, run2 = incl2 - local2;
     for (int j = 0; j < per; ++j) {
       const int e = lane * per + j;
       if (e < experts) {
         s_pre[e] = run;
+        s_pre2[e] = run2;
         const int32_t cnt = s_off[e + 1] - s_off[e];
-        run += cnt > 0 ? (cnt + S::BM - 1) / S::BM : 0;
+        run += full_tiles(cnt);
+        run2 += short_tiles(cnt);
       }
     }
-    if (lane == 63) s_pre[experts] = incl;
+    if (lane == 63) {
+      s_pre[experts] = incl;
+      s_pre2[experts] = incl2;
+    }
   }
   __syncthreads();
-  const int row_tiles = s_pre[experts];
+  const int full_rows = s_pre[experts];
+  const int short_rows = s_pre2[experts];
   const int col_tiles = (N + S::BN - 1) / S::BN;
-  const long total = static_cast<long>(row_tiles) * col_tiles;
+  const long total_full = static_cast<long>(full_rows) * col_tiles;
+  const long total = total_full + static_cast<long>(short_rows) * col_tiles;
 
   // Workgroups are dispatched round-robin over the XCDs; give the workgroups
   // of one XCD consecutive tile ids so their operands meet in the same L2.
@@ -290,23 +334,25 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
   const int b = static_cast<int>(blockIdx.x);
   const int worker = (grid % kXcds == 0) ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
 
-  const int wm0 = (wave / S::WN) * (S::BM / S::WM);
-  const int wn0 = (wave % S::WN) * (S::BN / S::WN);
   const int g = lane >> 4;
   const int li = lane & 15;
   const int nk = (K + S::BK - 1) / S::BK;
 
   for (long t = worker; t < total; t += grid) {
+    const bool is_short = t >= total_full;
+    const int32_t* pre = is_short ? s_pre2 : s_pre;
     int rt, ct;
-    decode_tile(static_cast<int>(t), row_tiles, col_tiles, &rt, &ct);
-    // expert = last e with s_pre[e] <= rt (binary search over the prefix)
+    decode_tile(static_cast<int>(is_short ? t - total_full : t), is_short ? short_rows : full_rows,
+                col_tiles, &rt, &ct);
+    // expert = last e with pre[e] <= rt (binary search over the prefix)
     int lo = 0, hi = experts - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (s_pre[mid] <= rt) lo = mid; else hi = mid - 1;
+      if (pre[mid] <= rt) lo = mid; else hi = mid - 1;
     }
     const int e = lo;
-    const int row0 = s_off[e] + (rt - s_pre[e]) * S::BM;
+    // a short tile is its expert's last: the rows past its full tiles
+    const int row0 = s_off[e] + (is_short ? (s_off[e + 1] - s_off[e]) / S::BM : rt - s_pre[e]) * S::BM;
     const int row_end = s_off[e + 1];
     const int n0 = ct * S::BN;
     const float* B = prm.W + static_cast<std::size_t>(kGroupedRows ? e : 0) * K * N;
@@ -329,92 +375,153 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
       __syncthreads();
       src_rows = s_src;
     }
-    const bool write_xp = MODE == kChainGrouped && ct == 0 && prm.x_permuted != nullptr;
+    // Gathered rows go to x_permuted spread over the column tiles: tile ct
+    // writes the k slices kt with kt % col_tiles == ct (every column tile
+    // loads all of the rows' k slices anyway).
+    const bool write_xp = MODE == kChainGrouped && prm.x_permuted != nullptr;
+    auto writes_slice = [&](int kt) { return write_xp && kt % col_tiles == ct; };
 
-    v4f acc[S::kTM][S::kTN];
+    // The tile's MFMA work, for one wave layout: TM x TN 16x16 tiles per wave
+    // starting at tile row wm0 and column wn0. Every layout accumulates each
+    // output in the same k order (slices ascending, 16-wide k chunks, one
+    // MFMA step per 4 k), so they give bit-identical results.
+    auto run_tile = [&](auto layout) {
+      using L = decltype(layout);
+      constexpr int TM = L::kTM;
+      constexpr int TN = L::kTN;
+      const int wm0 = L::wm0(wave);
+      const int wn0 = L::wn0(wave);
+      v4f acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < S::kTM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < S::kTN; ++j) acc[i][j] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
+        for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
 
-    Stage<S, VEC> st;
-    st.set_rows(prm.X, src_rows, row0, row_end, K, write_xp ? prm.x_permuted : nullptr, tid);
-    if (nk > 0) {
-      st.load(B, n0, N, K, 0, tid);
-      st.store(stages, tid);
-      if (write_xp) st.store_a_rows(K, 0, tid);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
-      if (S::kStages > 1 && kt + 1 < nk) {
-        st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
-      }
-      const float* As = cur;
-      const float* Bs = cur + S::BM * S::kLd;
+      // One BK slice from the LDS stage of slice kt into the accumulators.
+      auto multiply = [&](int kt) {
+        const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
+        const float* As = cur;
+        const float* Bs = cur + S::BM * S::kLd;
 #pragma unroll
-      for (int kk = 0; kk < S::BK; kk += 16) {
-        float4 af[S::kTM], bf[S::kTN];
+        for (int kk = 0; kk < S::BK; kk += 16) {
+          float4 af[TM], bf[TN];
 #pragma unroll
-        for (int i = 0; i < S::kTM; ++i) {
-          af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * S::kLd + kk + 4 * g);
-        }
+          for (int i = 0; i < TM; ++i) {
+            af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * S::kLd + kk + 4 * g);
+          }
 #pragma unroll
-        for (int j = 0; j < S::kTN; ++j) {
-          bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * S::kLd + kk + 4 * g);
-        }
+          for (int j = 0; j < TN; ++j) {
+            bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * S::kLd + kk + 4 * g);
+          }
 #pragma unroll
-        for (int i = 0; i < S::kTM; ++i) {
+          for (int i = 0; i < TM; ++i) {
 #pragma unroll
-          for (int j = 0; j < S::kTN; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+            for (int j = 0; j < TN; ++j) {
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+            }
           }
         }
-      }
-      if (S::kStages > 1 && kt + 1 < nk) {
-        st.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
-        if (write_xp) st.store_a_rows(K, (kt + 1) * S::BK, tid);
-      } else if (S::kStages == 1 && kt + 1 < nk) {
-        __syncthreads();  // every wave is done with the single stage
-        st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
-        st.store(stages, tid);
-        if (write_xp) st.store_a_rows(K, (kt + 1) * S::BK, tid);
-      }
-      __syncthreads();
-    }
-
-    // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
-#pragma unroll
-    for (int i = 0; i < S::kTM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rl = wm0 + i * 16 + 4 * g + r;
-        const int row = row0 + rl;
-        if (row >= row_end) continue;
-        float* yrow = prm.Y + static_cast<std::size_t>(row) * N;
-        float* comb = nullptr;
-        float w = 0.0F;
-        if constexpr (MODE == kChainGrouped) {
-          if (prm.y_out != nullptr) comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
-          w = s_w[rl];
+      };
+      Stage<S, VEC> st;
+      st.set_rows(prm.X, src_rows, row0, row_end, K, write_xp ? prm.x_permuted : nullptr, tid);
+      if constexpr (S::kStages > 1) {
+        // Two LDS stages fed from two register stages: slice kt + 2 is loaded
+        // while slice kt is multiplied, so each slice has two slices' compute
+        // time to arrive (the B slices of experts with few row tiles come from
+        // HBM rather than L2). The register stages swap roles every slice, so
+        // the loop runs two slices per trip (static roles, no copies).
+        Stage<S, VEC> st2 = st;
+        if (nk > 0) {
+          st.load(B, n0, N, K, 0, tid);
+          st.store(stages, tid);
+          if (writes_slice(0)) st.store_a_rows(K, 0, tid);
+          if (nk > 1) st2.load(B, n0, N, K, S::BK, tid);
         }
+        __syncthreads();
+        // held: slice kt (stored to LDS); next: slice kt + 1 (in flight)
+        auto step = [&](int kt, Stage<S, VEC>& held, Stage<S, VEC>& next) {
+          if (kt + 2 < nk) held.load(B, n0, N, K, (kt + 2) * S::BK, tid);
+          multiply(kt);
+          if (kt + 1 < nk) {
+            next.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
+            if (writes_slice(kt + 1)) next.store_a_rows(K, (kt + 1) * S::BK, tid);
+          }
+          __syncthreads();
+        };
+        for (int kt = 0; kt < nk; kt += 2) {
+          step(kt, st, st2);
+          if (kt + 1 < nk) step(kt + 1, st2, st);
+        }
+      } else {
+        if (nk > 0) {
+          st.load(B, n0, N, K, 0, tid);
+          st.store(stages, tid);
+          if (writes_slice(0)) st.store_a_rows(K, 0, tid);
+        }
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+          multiply(kt);
+          if (kt + 1 < nk) {
+            __syncthreads();  // every wave is done with the single stage
+            st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
+            st.store(stages, tid);
+            if (writes_slice(kt + 1)) st.store_a_rows(K, (kt + 1) * S::BK, tid);
+          }
+          __syncthreads();
+        }
+      }
+
+      // Epilogue: acc[i][j][r] is D[4g + r][li] of the 16x16 tile (i, j).
 #pragma unroll
-        for (int j = 0; j < S::kTN; ++j) {
-          const int col = n0 + wn0 + j * 16 + li;
-          if (col < N) {
-            yrow[col] = acc[i][j][r];
-            if constexpr (MODE == kChainGrouped) {
-              // Both routes of a token add into the zeroed output: fl(0 + a) + b
-              // is the same in either order, so the combine is deterministic
-              // and equals the rank-order unpermute.
-              if (comb != nullptr) unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rl = wm0 + i * 16 + 4 * g + r;
+          const int row = row0 + rl;
+          if (row >= row_end) continue;
+          float* yrow = prm.Y + static_cast<std::size_t>(row) * N;
+          float* comb = nullptr;
+          float w = 0.0F;
+          if constexpr (MODE == kChainGrouped) {
+            if (prm.y_out != nullptr) comb = prm.y_out + static_cast<std::size_t>(s_src[rl]) * N;
+            w = s_w[rl];
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn0 + j * 16 + li;
+            if (col < N) {
+              yrow[col] = acc[i][j][r];
+              if constexpr (MODE == kChainGrouped) {
+                // Both routes of a token add into the zeroed output: fl(0 + a) + b
+                // is the same in either order, so the combine is deterministic
+                // and equals the rank-order unpermute.
+                if (comb != nullptr) unsafeAtomicAdd(comb + col, __fmul_rn(w, acc[i][j][r]));
+              }
             }
           }
         }
       }
+    };
+    // Tile rows past the expert's end are padding: a tile with at most 64,
+    // 32 or 16 rows gives each of the four waves a 32-column slab of that
+    // height instead of the 2 x 2 layout of 64 x 64, so the padding costs no
+    // MFMA work beyond the 16-row granule and every SIMD stays busy.
+    if constexpr (kSlabs) {
+      const int rows = row_end - row0;
+      if (rows > 64) {
+        run_tile(WaveLayout<S::kTM, S::kTN, S>{});
+      } else if (rows > 32) {
+        run_tile(SlabLayout<4, 2, 32>{});
+      } else if (rows > 16) {
+        run_tile(SlabLayout<2, 2, 32>{});
+      } else {
+        run_tile(SlabLayout<1, 2, 32>{});
+      }
+    } else {
+      run_tile(WaveLayout<S::kTM, S::kTN, S>{});
     }
   }
 }
@@ -466,7 +573,7 @@ hipError_t launch_gemm(const GemmParams& prm, long tile_bound, hipStream_t strea
   if (grid >= kXcds) grid = grid / kXcds * kXcds;
   if (grid < 1) grid = 1;
   const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) +
-                          2 * static_cast<std::size_t>(prm.experts + 1) * sizeof(int32_t) +
+                          3 * static_cast<std::size_t>(prm.experts + 1) * sizeof(int32_t) +
                           2 * static_cast<std::size_t>(S::BM) * sizeof(int32_t);
   const dim3 g(static_cast<unsigned>(grid));
   return vec ? launch_one<S, true, MODE>(g, lds, prm, stream)
