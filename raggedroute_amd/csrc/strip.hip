@@ -138,12 +138,12 @@ __device__ __forceinline__ void seg_scan(SegTable& t, int nblk) {
   t.total_strips = carry_strips;
 }
 
-// Value of a per-lane table column for the uniform segment e.
-__device__ __forceinline__ int32_t seg_field(const int32_t (&col)[kMaxBlocks], int e) {
+// Value of a per-lane table column for the uniform segment e (< 64 nblk).
+__device__ __forceinline__ int32_t seg_field(const int32_t (&col)[kMaxBlocks], int nblk, int e) {
   int32_t v = 0;
 #pragma unroll
   for (int j = 0; j < kMaxBlocks; ++j) {
-    if (j == (e >> 6)) v = __builtin_amdgcn_readlane(col[j], e & 63);
+    if (j < nblk && j == (e >> 6)) v = __builtin_amdgcn_readlane(col[j], e & 63);
   }
   return v;
 }
@@ -244,16 +244,16 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
         break;
       }
     }
-    const int first = seg_field(wpre, e);
-    const int pre_e = seg_field(t.pre, e);
-    const int cnt_e = seg_field(t.cnt, e);
+    const int first = seg_field(wpre, nblk, e);
+    const int pre_e = seg_field(t.pre, nblk, e);
+    const int cnt_e = seg_field(t.cnt, nblk, e);
     const int end_e = pre_e + strips_of(cnt_e);
     r.s0 = pre_e + (worker - first) * m;
     r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
     if (r.s0 > r.s1) r.s0 = r.s1;
     r.e = e;
     r.pre = pre_e;
-    r.off = seg_field(t.off, e);
+    r.off = seg_field(t.off, nblk, e);
     r.cnt = cnt_e;
   }
   return r;
@@ -269,10 +269,10 @@ struct StripInfo {
 __device__ __forceinline__ StripInfo strip_info(const SegTable& t, int nblk, int segments, int s) {
   StripInfo si;
   si.e = seg_find(t, nblk, segments, s);
-  const int off = seg_field(t.off, si.e);
-  si.rank0 = (s - seg_field(t.pre, si.e)) * kRows;
+  const int off = seg_field(t.off, nblk, si.e);
+  si.rank0 = (s - seg_field(t.pre, nblk, si.e)) * kRows;
   si.row0 = off + si.rank0;
-  si.row_end = off + seg_field(t.cnt, si.e);
+  si.row_end = off + seg_field(t.cnt, nblk, si.e);
   return si;
 }
 
@@ -286,7 +286,9 @@ constexpr int strip_waves(int bn, int mode) {
   return mode == kStripRouterGate ? bn / 16 : (bn == 128 ? kWaves128 : 4);
 }
 
-template <int BN, int WAVES, int MODE, int CHUNKS>
+// NB: segment blocks of 64 the launch may hold (1: segments <= 64, the
+// scheduling tables fold to one register column; else kMaxBlocks).
+template <int BN, int WAVES, int MODE, int CHUNKS, int NB>
 __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParams p) {
   constexpr int kWaves = WAVES;
   constexpr int kTiles = BN / 16 / WAVES;              // 16-column MFMA tiles per wave
@@ -303,7 +305,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   const int K = p.K;
   const int N = p.N;
   const int E = p.segments;
-  const int nblk = (E + 63) >> 6;
+  static_assert(NB == 1 || NB == kMaxBlocks, "one block or all");
+  const int nblk = NB == 1 ? 1 : (E + 63) >> 6;
   const int chunks = CHUNKS > 0 ? CHUNKS : (K + 15) >> 4;
   const int kLd = chunks * 16 + 4;
   float* As2 = lds;               // [2][16][kLd]: A rows of strip s in buffer s & 1
@@ -336,13 +339,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // N read column N - 1 (their outputs are never stored); rows past K are
   // zero (lanes masked off the load keep the zero: no wait for the data).
   float bq[kMaxChunks][4];
-  auto load_b = [&](int e) {
+  auto load_b = [&](int e, int c_lo = 0, int c_hi = kMaxChunks) {
     const float* W = p.W + static_cast<std::size_t>(e) * K * N;
     const int n = 16 * wave + li;
     const int nc = n < N ? n : N - 1;
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
-      if (c < chunks) {
+      if (c < chunks && c >= c_lo && c < c_hi) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int k = 16 * c + 4 * g + s;  // (k * N < 2^31: K <= 256, N <= 128)
@@ -466,7 +469,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
           p.offsets_out[e] = tab.off[j];
         }
       }
-      if (lane == 0) p.offsets_out[E] = seg_field(tab.off, E - 1) + seg_field(tab.cnt, E - 1);
+      if (lane == 0) p.offsets_out[E] = seg_field(tab.off, nblk, E - 1) + seg_field(tab.cnt, nblk, E - 1);
     }
   }
 
@@ -493,6 +496,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   };
   StripInfo cur{};
   if (s0 < s1) cur = info(s0);
+  if constexpr (MODE == kStripChain) {
+    // The first half of B (k chunks 0..7, 32 loads per lane) as soon as the
+    // first segment is known: it arrives while the ranks are computed. All of
+    // B here would reach the wave's limit of outstanding loads (63) and stall
+    // the rank passes at issue (measured at the headline shape: expert launch
+    // 19.6 us with all of B here, 18.5 us with half, 18.7 us with none).
+    if (s0 < s1) load_b(cur.e, 0, 8);
+  }
   if constexpr (MODE == kStripChain) {
     // Every strip's info, once and in parallel (wave w: strips s0 + w,
     // s0 + w + waves, ...), for the strip loop to read back from LDS (read
@@ -538,8 +549,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
 #pragma unroll 1
       for (int s = s0; s < s1 && nseg < kMaxSegs; ++nseg) {
         const int e = seg_find(tab, nblk, E, s);
-        const int pre_e = seg_field(tab.pre, e);
-        const int rows_e = seg_field(tab.cnt, e);
+        const int pre_e = seg_field(tab.pre, nblk, e);
+        const int rows_e = seg_field(tab.cnt, nblk, e);
         const int end_e = pre_e + strips_of(rows_e);
         const int last = s1 < end_e ? s1 : end_e;
         const int hi = (last - pre_e) * kRows;
@@ -685,14 +696,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   StripInfo prev{};
   bool pending = false;
 
-  // Issue order: the first strip's A rows, the route map's weight loads,
-  // B, then the route map's stores. Memory operations complete in order, so
-  // the A stage waits for A and the weights alone, and the first strip's
-  // MFMAs wait for B one k chunk at a time. At K > 224 B is more loads per
-  // lane (4 per k chunk) than a wave may have outstanding (63): the wave
-  // stalls at issue until B starts to arrive, so B then follows the route
-  // map's stores instead (measured at K = 256: expert launch 18.6 us against
-  // 19.6 us; at K = 128 B before the stores is faster).
+  // Issue order (chain): the first half of B (above), the first strip's A
+  // rows, the route map's weight loads and stores, then the rest of B.
+  // Memory operations complete in order, so the A stage waits for the first
+  // half of B, A and the weights, and the first strip's MFMAs wait for the
+  // rest of B one k chunk at a time. Other modes: A rows, then all of B.
   int src = -1;
   if (s0 < s1) {
     src = a_source(s0, cur);
@@ -701,11 +709,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   if constexpr (MODE == kStripChain) {
     // Route map entries of my rows; the route weights are loaded now and
     // stored to LDS with the first strip's A rows.
-    const bool b_early = 4 * chunks < 60;
     const bool mine = tid < (s1 - s0) * kRows;  // <= (kMaxSegs + 1) * 16 <= kThreads
     const int32_t route = mine ? s_slot[tid] : -1;
     if (route >= 0 && p.combine) w_pending = p.route_weights[route];
-    if (s0 < s1 && b_early) load_b(cur.e);
     if (mine) {
       // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
       const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
@@ -715,7 +721,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
       }
     }
-    if (s0 < s1 && !b_early) load_b(cur.e);
+    if (s0 < s1) load_b(cur.e, 8, kMaxChunks);  // the rest of B
   } else {
     if (s0 < s1) load_b(cur.e);
   }
@@ -903,13 +909,21 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   return bytes;
 }
 
+template <int BN, int MODE, int CHUNKS, int NB>
+hipError_t launch_strip_4(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
+  constexpr int kWaves = strip_waves(BN, MODE);
+  const hipError_t attr = allow_lds(rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS, NB>);
+  if (attr != hipSuccess) return attr;
+  rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS, NB><<<grid, kWaves * 64, lds, stream>>>(p);
+  return hipGetLastError();
+}
+
 template <int BN, int MODE, int CHUNKS>
 hipError_t launch_strip_3(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
-  constexpr int kWaves = strip_waves(BN, MODE);
-  const hipError_t attr = allow_lds(rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS>);
-  if (attr != hipSuccess) return attr;
-  rr_strip_gemm_kernel<BN, kWaves, MODE, CHUNKS><<<grid, kWaves * 64, lds, stream>>>(p);
-  return hipGetLastError();
+  if constexpr (MODE == kStripGrouped || MODE == kStripChain) {
+    if (p.segments > 64) return launch_strip_4<BN, MODE, CHUNKS, kMaxBlocks>(p, grid, lds, stream);
+  }
+  return launch_strip_4<BN, MODE, CHUNKS, 1>(p, grid, lds, stream);
 }
 
 template <int BN, int MODE>
