@@ -64,8 +64,9 @@ def parse(argv=None):
     # shape-generic runner (reference benchmarks/benchmark_main.cpp:16-33)
     ap.add_argument("--suite", choices=SUITES, help="runner mode: time one chain entry at --param shapes")
     ap.add_argument("--operator", choices=OPERATORS, help="runner mode: time one operator at --param shapes")
-    ap.add_argument("--param", action="append", default=[], metavar="KEY=VALUE",
-                    help="T, E, K, N, top_k, distribution, zipf_s, tie_fraction, seed")
+    ap.add_argument("--param", action="extend", nargs="+", default=[], metavar="KEY=VALUE",
+                    help="T, E, K, N, top_k, distribution, zipf_s, tie_fraction, seed "
+                         "(one or more pairs per flag, the flag repeatable)")
     ap.add_argument("--variant", default="auto", choices=["auto", "naive", "optimized"])
     ap.add_argument("--cache-mode", default="warm", choices=["warm", "cold_scrub"])
     ap.add_argument("--cache-scrub-bytes", type=int, default=512 << 20)
