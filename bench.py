@@ -533,13 +533,14 @@ def c5(torch, device, steps=20, cpu_sample=False):
     return out
 
 
-def cpu_sample_c4(ch, expert_weights, routes, rows=8):
-    """C4 grouped GEMM on the oracle (single thread) over `rows` rows of
-    x_permuted spread evenly over its R rows (the full 1.9 TFLOP is out of
-    reach on one core), extrapolated linearly to all R rows."""
+def cpu_sample_c4(ch, expert_weights, routes, rows=41):
+    """C4 grouped GEMM on the oracle (single thread) over a seeded sample of
+    `rows` rows of x_permuted (0.25 % of R: the measurement plan's 1 % would be
+    about 50 s of CPU time here, the full 1.9 TFLOP is out of reach on one
+    core), extrapolated linearly to all R rows."""
     import oracle
     offsets = ch.offsets.cpu().numpy().astype(np.int64)
-    pick = np.linspace(0, routes - 1, rows).astype(np.int64)
+    pick = np.sort(np.random.default_rng(0).choice(routes, size=rows, replace=False)).astype(np.int64)
     xs = ch.xp[torch_index(pick, ch.xp.device)].cpu().numpy()
     expert = np.searchsorted(offsets, pick, side="right") - 1
     offs = np.searchsorted(expert, np.arange(len(offsets)), side="left").astype(np.int32)
@@ -549,26 +550,28 @@ def cpu_sample_c4(ch, expert_weights, routes, rows=8):
     sec = time.perf_counter() - t0
     flops = 2.0 * rows * w.shape[1] * w.shape[2]
     return {"kind": "port", "cores": 1,
-            "sample": f"{rows} of {routes} x_permuted rows (evenly spaced) through the oracle grouped GEMM "
-                      "(single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
+            "sample": f"{rows} of {routes} x_permuted rows (seeded random sample, seed 0) through the oracle "
+                      "grouped GEMM (single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
             "sample_ms": round(sec * 1e3, 3), "gflops": round(flops / sec / 1e9, 3),
             "extrapolated_grouped_gemm_ms": round(sec * routes / rows * 1e3, 1)}
 
 
 def cpu_sample_c5(inputs, cfg, frac=100):
-    """C5 chain_from_tokens on the oracle (single thread) over the first 1 % of
-    the tokens (the full chain is 112 GFLOP scalar), extrapolated linearly."""
+    """C5 chain_from_tokens on the oracle (single thread) over a seeded 1 %
+    sample of the tokens (the full chain is 112 GFLOP scalar), extrapolated
+    linearly."""
     import oracle
     n = max(1, cfg.tokens // frac)
-    x = inputs["x"][:n].cpu().numpy()
+    pick = np.sort(np.random.default_rng(0).choice(cfg.tokens, size=n, replace=False))
+    x = inputs["x"][torch_index(pick, inputs["x"].device)].cpu().numpy()
     rw = inputs["router_weights"].cpu().numpy()
     we = inputs["expert_weights"].cpu().numpy()
     t0 = time.perf_counter()
     oracle.chain(x, we, router_weights=rw)
     sec = time.perf_counter() - t0
     return {"kind": "port", "cores": 1,
-            "sample": f"first {n} of {cfg.tokens} tokens through the oracle chain_from_tokens "
-                      "(single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
+            "sample": f"{n} of {cfg.tokens} tokens (seeded random sample, seed 0) through the oracle "
+                      "chain_from_tokens (single thread, -O2 -ffp-contract=off); full time extrapolated linearly",
             "sample_ms": round(sec * 1e3, 3), "tokens_per_s": round(n / sec, 1),
             "extrapolated_chain_ms": round(sec * cfg.tokens / n * 1e3, 1)}
 
