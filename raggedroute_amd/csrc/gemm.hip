@@ -223,6 +223,30 @@ struct Stage {
   }
 };
 
+// Direct global -> LDS staging (gfx950 global_load_lds_dwordx4) for the
+// 128 x 128 x 32 tile when K is a multiple of 32: one wave instruction fills
+// one contiguous KiB of LDS, lane L the 16 bytes at L * 16, so the layouts are
+// chosen by which global chunk each lane fetches. No staging registers, no LDS
+// store instructions, no transposition.
+//   A stage [128 rows][8 slots of 4 k]: slot s of row r holds k chunk
+//     s ^ swa(r). A lane of an MFMA operand read takes row r = base + li and
+//     one k chunk: the 16 rows of a lane group land in 16 distinct 16-byte
+//     bank groups (and any 8 consecutive rows in 8).
+//   B stage [32 k rows][32 slots of 4 n] (B's own row-major order): slot s of
+//     row k holds n chunk s ^ swb(k). An operand read takes one float per lane
+//     at rows k = kk + 4g + s: the four lane groups read XOR-separated chunks,
+//     64 distinct banks, and rows s, s + 1 pair into one ds_read2st64_b32.
+// The MFMA k order is the register-staged kernel's (k = kk + 4g + s at step s),
+// so both staging paths give bit-identical products.
+struct DmaLayout {
+  static constexpr int kRowsA = 128, kBK = 32, kColsB = 128;
+  static constexpr int kAFloats = kRowsA * kBK;   // 4096
+  static constexpr int kStageFloats = kAFloats + kBK * kColsB;  // 8192 = 32 KiB
+  static constexpr int kBlockFloats = 256;         // one wave instruction: 64 lanes x 16 B
+  __device__ static int swa(int r) { return (r ^ (r >> 3)) & 7; }
+  __device__ static int swb(int k) { return 4 * ((k >> 2) & 3); }
+};
+
 // Tile space decode: row tiles are grouped kGroupM at a time so that workgroups
 // running together share both A row blocks and B column strips.
 __device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles, int* rt, int* ct) {
@@ -253,14 +277,16 @@ struct SlabLayout {
   __device__ static int wn0(int wave) { return wave * COLS; }
 };
 
-template <class S, bool VEC, int MODE>
+template <class S, bool VEC, int MODE, bool DMA>
 __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams prm) {
   constexpr bool kGroupedRows = MODE == kGrouped || MODE == kChainGrouped;
   // slab layouts for tiles of at most 64 rows (the 128 x 128 tile, 2 x 2 waves)
   constexpr bool kSlabs = S::BM == 128 && S::BN == 128 && S::WM == 2 && S::WN == 2;
+  static_assert(!DMA || (kSlabs && S::BK == DmaLayout::kBK && VEC), "DMA staging: the 128 x 128 x 32 tile");
+  constexpr int kStageFloats = DMA ? DmaLayout::kStageFloats : S::kStageFloats;
   extern __shared__ float lds[];
-  float* stages = lds;                                                              // kStages
-  int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * S::kStageFloats);  // [E + 1]
+  float* stages = lds;                                                             // kStages
+  int32_t* s_off = reinterpret_cast<int32_t*>(lds + S::kStages * kStageFloats);  // [E + 1]
   int32_t* s_pre = s_off + prm.experts + 1;   // [E + 1] full row tiles before expert e
   int32_t* s_pre2 = s_pre + prm.experts + 1;  // [E + 1] short row tiles before expert e
   int32_t* s_src = s_pre2 + prm.experts + 1;  // [BM] chain: token row of X per tile row
@@ -399,7 +425,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
 
       // One BK slice from the LDS stage of slice kt into the accumulators.
       auto multiply = [&](int kt) {
-        const float* cur = stages + (kt % S::kStages) * S::kStageFloats;
+        const float* cur = stages + (kt % S::kStages) * kStageFloats;
         const float* As = cur;
         const float* Bs = cur + S::BM * S::kLd;
 #pragma unroll
@@ -425,52 +451,196 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
           }
         }
       };
-      Stage<S, VEC> st;
-      st.set_rows(prm.X, src_rows, row0, row_end, K, write_xp ? prm.x_permuted : nullptr, tid);
-      if constexpr (S::kStages > 1) {
-        // Two LDS stages fed from two register stages: slice kt + 2 is loaded
-        // while slice kt is multiplied, so each slice has two slices' compute
-        // time to arrive (the B slices of experts with few row tiles come from
-        // HBM rather than L2). The register stages swap roles every slice, so
-        // the loop runs two slices per trip (static roles, no copies).
-        Stage<S, VEC> st2 = st;
-        if (nk > 0) {
-          st.load(B, n0, N, K, 0, tid);
-          st.store(stages, tid);
-          if (writes_slice(0)) st.store_a_rows(K, 0, tid);
-          if (nk > 1) st2.load(B, n0, N, K, S::BK, tid);
-        }
-        __syncthreads();
-        // held: slice kt (stored to LDS); next: slice kt + 1 (in flight)
-        auto step = [&](int kt, Stage<S, VEC>& held, Stage<S, VEC>& next) {
-          if (kt + 2 < nk) held.load(B, n0, N, K, (kt + 2) * S::BK, tid);
-          multiply(kt);
-          if (kt + 1 < nk) {
-            next.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
-            if (writes_slice(kt + 1)) next.store_a_rows(K, (kt + 1) * S::BK, tid);
+      if constexpr (DMA) {
+        using D = DmaLayout;
+        const int rows = row_end - row0 < S::BM ? row_end - row0 : S::BM;
+        // This thread's chunk of each of the wave's four A and four B blocks
+        // (block q = 4 p + wave: A rows 8q .. 8q + 7, B k rows 2q, 2q + 1).
+        // A rows without a source read row 0 of the tile's source (their
+        // products land in output rows that are never stored); B columns past
+        // N read the last chunk of the row (likewise never stored).
+        const float* asrc[4];
+        const float* bsrc[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int q = 4 * p + wave;
+          const int r = 8 * q + (lane >> 3);
+          const int kc = (lane & 7) ^ D::swa(r);
+          int src = -1;
+          if constexpr (MODE == kChainGrouped) {
+            src = s_src[r];
+          } else {
+            src = r < rows ? row0 + r : -1;
           }
+          if (src < 0) src = MODE == kChainGrouped ? 0 : row0;
+          asrc[p] = prm.X + static_cast<std::size_t>(src) * K + 4 * kc;
+          const int kl = 2 * q + (lane >> 5);
+          const int n = n0 + 4 * ((lane & 31) ^ D::swb(kl));
+          bsrc[p] = B + static_cast<std::size_t>(kl) * N + (n < N ? n : N - 4);
+        }
+        const std::size_t b_slice = static_cast<std::size_t>(D::kBK) * N;
+        // Slice kt -> LDS stage kt & 1 (every block, also past a short tile's
+        // rows: a branch here would split the slice's code and its waits).
+        auto issue = [&](int kt, float* As) {
+          float* Bs = As + D::kAFloats;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int q = 4 * p + wave;
+            __builtin_amdgcn_global_load_lds(asrc[p] + kt * D::kBK, As + q * D::kBlockFloats, 16, 0, 0);
+          }
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int q = 4 * p + wave;
+            __builtin_amdgcn_global_load_lds(bsrc[p] + kt * b_slice, Bs + q * D::kBlockFloats, 16, 0, 0);
+          }
+        };
+        // Operand addresses inside a stage. A: row r = wm0 + 16 i + li, k
+        // chunk kk / 4 + g at slot (kk / 4 + g) ^ swa(r). B: row k = kk + 4g + s,
+        // column n = wn0 + 16 j + li at (kk + s) * 128 + boff[j] (swb(k) = 4g).
+        int aoff[TM][2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = wm0 + 16 * i + li;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) aoff[i][h] = r * D::kBK + 4 * ((4 * h + g) ^ D::swa(r));
+        }
+        int boff[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = wn0 + 16 * j + li;
+          boff[j] = 4 * g * D::kColsB + 4 * ((n >> 2) ^ (4 * g)) + (n & 3);
+        }
+        // One slice: the first half's operands are read, the next slice's
+        // loads issued, then the MFMAs run with the second half's reads among
+        // them. (The reads come first so that the loads of the next slice,
+        // which write the other stage, are never ordered before them.)
+        // (restrict: the stage read and the stage loaded are disjoint, which
+        // lets the compiler leave the reads after the loads unwaited)
+        auto multiply_dma = [&](int kt, const float* __restrict__ As, float* __restrict__ next) {
+          const float* Bs = As + D::kAFloats;
+          float4 af[2][TM];
+          float bf[2][TN][4];
+          auto read = [&](int h) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const float4*>(As + aoff[i][h]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+#pragma unroll
+              for (int s = 0; s < 4; ++s) bf[h][j][s] = Bs[(16 * h + s) * D::kColsB + boff[j]];
+            }
+          };
+          read(0);
+          // (the last slice loads itself again into the unused stage: no
+          // branch in the slice, whose waits then stay per operand)
+          issue(kt + 1 < nk ? kt + 1 : kt, next);
+          read(1);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+              for (int j = 0; j < TN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].x, bf[h][j][0], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].y, bf[h][j][1], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].z, bf[h][j][2], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].w, bf[h][j][3], acc[i][j], 0, 0, 0);
+              }
+            }
+          }
+          // Issue order: the first half's reads, then the next slice's loads
+          // and the second half's reads spread over the first half's MFMAs.
+          __builtin_amdgcn_sched_group_barrier(0x100, TM + 2 * TN, 0);  // LDS reads
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load into LDS
+          }
+#pragma unroll
+          for (int r = 0; r < TM + 2 * TN; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);  // three MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          }
+        };
+        // chain: the gathered rows of slice kt, read back from LDS, go to x_permuted
+        auto store_xp = [&](int kt, const float* As) {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int f = tid + p * S::kThreads;  // chunk f: row f / 8, slot f % 8
+            const int r = f >> 3;
+            if (r < rows) {
+              const int kc = (f & 7) ^ D::swa(r);
+              const float4 v = *reinterpret_cast<const float4*>(As + 4 * f);
+              *reinterpret_cast<float4*>(prm.x_permuted + static_cast<std::size_t>(row0 + r) * K +
+                                         kt * D::kBK + 4 * kc) = v;
+            }
+          }
+        };
+        // Slice kt + 1 streams into the other stage while slice kt is
+        // multiplied; the barrier after each slice (which waits for the wave's
+        // own LDS loads first) makes it visible and frees the stage just read.
+        auto slice = [&](int kt, float* cur, float* next) {
+          if (writes_slice(kt)) store_xp(kt, cur);
+          multiply_dma(kt, cur, next);
+          // (the MFMAs stay ahead of the wait: moved past it, they would idle
+          // behind the loads of the next slice)
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of slice kt + 1
           __syncthreads();
         };
-        for (int kt = 0; kt < nk; kt += 2) {
-          step(kt, st, st2);
-          if (kt + 1 < nk) step(kt + 1, st2, st);
-        }
-      } else {
-        if (nk > 0) {
-          st.load(B, n0, N, K, 0, tid);
-          st.store(stages, tid);
-          if (writes_slice(0)) st.store_a_rows(K, 0, tid);
-        }
+        if (nk > 0) issue(0, stages);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         for (int kt = 0; kt < nk; ++kt) {
-          multiply(kt);
-          if (kt + 1 < nk) {
-            __syncthreads();  // every wave is done with the single stage
-            st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
+          slice(kt, stages + (kt & 1) * kStageFloats, stages + ((kt + 1) & 1) * kStageFloats);
+        }
+      } else {
+        Stage<S, VEC> st;
+        st.set_rows(prm.X, src_rows, row0, row_end, K, write_xp ? prm.x_permuted : nullptr, tid);
+        if constexpr (S::kStages > 1) {
+          // Two LDS stages fed from two register stages: slice kt + 2 is loaded
+          // while slice kt is multiplied, so each slice has two slices' compute
+          // time to arrive (the B slices of experts with few row tiles come from
+          // HBM rather than L2). The register stages swap roles every slice, so
+          // the loop runs two slices per trip (static roles, no copies).
+          Stage<S, VEC> st2 = st;
+          if (nk > 0) {
+            st.load(B, n0, N, K, 0, tid);
             st.store(stages, tid);
-            if (writes_slice(kt + 1)) st.store_a_rows(K, (kt + 1) * S::BK, tid);
+            if (writes_slice(0)) st.store_a_rows(K, 0, tid);
+            if (nk > 1) st2.load(B, n0, N, K, S::BK, tid);
           }
           __syncthreads();
+          // held: slice kt (stored to LDS); next: slice kt + 1 (in flight)
+          auto step = [&](int kt, Stage<S, VEC>& held, Stage<S, VEC>& next) {
+            if (kt + 2 < nk) held.load(B, n0, N, K, (kt + 2) * S::BK, tid);
+            multiply(kt);
+            if (kt + 1 < nk) {
+              next.store(stages + ((kt + 1) % S::kStages) * S::kStageFloats, tid);
+              if (writes_slice(kt + 1)) next.store_a_rows(K, (kt + 1) * S::BK, tid);
+            }
+            __syncthreads();
+          };
+          for (int kt = 0; kt < nk; kt += 2) {
+            step(kt, st, st2);
+            if (kt + 1 < nk) step(kt + 1, st2, st);
+          }
+        } else {
+          if (nk > 0) {
+            st.load(B, n0, N, K, 0, tid);
+            st.store(stages, tid);
+            if (writes_slice(0)) st.store_a_rows(K, 0, tid);
+          }
+          __syncthreads();
+          for (int kt = 0; kt < nk; ++kt) {
+            multiply(kt);
+            if (kt + 1 < nk) {
+              __syncthreads();  // every wave is done with the single stage
+              st.load(B, n0, N, K, (kt + 1) * S::BK, tid);
+              st.store(stages, tid);
+              if (writes_slice(kt + 1)) st.store_a_rows(K, (kt + 1) * S::BK, tid);
+            }
+            __syncthreads();
+          }
         }
       }
 
@@ -556,12 +726,20 @@ hipError_t allow_full_lds(Kernel kernel) {
   return status;
 }
 
-template <class S, bool VEC, int MODE>
+template <class S, bool VEC, int MODE, bool DMA>
 hipError_t launch_one(dim3 grid, std::size_t lds, const GemmParams& prm, hipStream_t stream) {
-  const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, MODE>);
+  const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, MODE, DMA>);
   if (attr != hipSuccess) return attr;
-  rr_gemm_mfma_kernel<S, VEC, MODE><<<grid, S::kThreads, lds, stream>>>(prm);
+  rr_gemm_mfma_kernel<S, VEC, MODE, DMA><<<grid, S::kThreads, lds, stream>>>(prm);
   return hipGetLastError();
+}
+
+// Staging override for tests and A/B runs: RR_GEMM_STAGING=registers keeps the
+// register-staged path where the direct LDS loads would otherwise run. Read at
+// every launch (one getenv).
+bool registers_forced() {
+  const char* v = std::getenv("RR_GEMM_STAGING");
+  return v != nullptr && std::strcmp(v, "registers") == 0;
 }
 
 template <class S, int MODE>
@@ -572,12 +750,19 @@ hipError_t launch_gemm(const GemmParams& prm, long tile_bound, hipStream_t strea
   long grid = tile_bound < cap ? tile_bound : cap;
   if (grid >= kXcds) grid = grid / kXcds * kXcds;
   if (grid < 1) grid = 1;
-  const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) +
-                          3 * static_cast<std::size_t>(prm.experts + 1) * sizeof(int32_t) +
-                          2 * static_cast<std::size_t>(S::BM) * sizeof(int32_t);
+  const std::size_t meta = 3 * static_cast<std::size_t>(prm.experts + 1) * sizeof(int32_t) +
+                           2 * static_cast<std::size_t>(S::BM) * sizeof(int32_t);
   const dim3 g(static_cast<unsigned>(grid));
-  return vec ? launch_one<S, true, MODE>(g, lds, prm, stream)
-             : launch_one<S, false, MODE>(g, lds, prm, stream);
+  if constexpr (S::BM == 128 && S::BN == 128 && S::WM == 2 && S::WN == 2 && S::BK == DmaLayout::kBK) {
+    // whole 32-deep slices and 16-byte rows: direct LDS loads
+    if (vec && prm.K % DmaLayout::kBK == 0 && !registers_forced()) {
+      const std::size_t lds = S::kStages * DmaLayout::kStageFloats * sizeof(float) + meta;
+      return launch_one<S, true, MODE, true>(g, lds, prm, stream);
+    }
+  }
+  const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) + meta;
+  return vec ? launch_one<S, true, MODE, false>(g, lds, prm, stream)
+             : launch_one<S, false, MODE, false>(g, lds, prm, stream);
 }
 
 // 128x128, four 64x64 waves, BK 32: large problems (C4, C5 grouped). (BK 16,

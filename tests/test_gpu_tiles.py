@@ -1,9 +1,11 @@
 """Every GEMM kernel configuration gives the same bits: the strip kernels and
 each tiled configuration forced through RR_GEMM_TILE (read by the library at
-every launch) accumulate each output in the same k order (16-wide k chunks in
-ascending order, one MFMA step per 4 k), so dense and grouped outputs must be
-bit-identical to the default dispatch, and within the accumulation-aware bound
-of the float64 product. Shapes cover aligned (vector loads) and odd K / N or
+every launch), and the large tile with its slices staged through registers
+instead of loaded straight into LDS (RR_GEMM_STAGING=registers), accumulate
+each output in the same k order (16-wide k chunks in ascending order, one MFMA
+step per 4 k), so dense and grouped outputs must be bit-identical to the
+default dispatch, and within the accumulation-aware bound of the float64
+product. Shapes cover aligned (vector loads) and odd K / N or
 offset pointers (scalar loads), ragged and empty segments and the K tails of
 the 16- and 64-deep slices.
 """
@@ -19,20 +21,29 @@ from test_gpu_ops import NATIVE, check_grouped, gemm_ok, ok, run_grouped
 
 pytestmark = pytest.mark.gpu
 
-TILES = ["large", "small", "medium", "narrow", "small256", "medium256", "narrow256"]
+# "large/registers": the large tile with register-staged slices where the
+# direct LDS loads (K a multiple of 32, 16-byte rows) would otherwise run
+TILES = ["large", "large/registers", "small", "medium", "narrow", "small256", "medium256",
+         "narrow256"]
 
 
 @pytest.fixture()
 def tile_env():
-    saved = os.environ.get("RR_GEMM_TILE")
+    saved = {v: os.environ.get(v) for v in ("RR_GEMM_TILE", "RR_GEMM_STAGING")}
+
+    def put(var, value):
+        if value is None:
+            os.environ.pop(var, None)
+        else:
+            os.environ[var] = value
 
     def set_tile(name):
-        if name is None:
-            os.environ.pop("RR_GEMM_TILE", None)
-        else:
-            os.environ["RR_GEMM_TILE"] = name
+        tile, _, staging = (name or "").partition("/")
+        put("RR_GEMM_TILE", tile or None)
+        put("RR_GEMM_STAGING", staging or None)
     yield set_tile
-    set_tile(saved)
+    for var, value in saved.items():
+        put(var, value)
 
 
 GROUPED = [
@@ -42,6 +53,7 @@ GROUPED = [
     ([7, 0, 12, 1, 0], 33, 17, 0),                    # scalar loads (K, N odd)
     ([40, 0, 3, 90], 96, 40, 1),                      # offset pointers
     ([200, 129, 64], 300, 136, 0),                    # K past 256, N past 128
+    ([200, 129, 64, 0, 250], 320, 136, 0),            # whole 32-deep slices, N past 128
 ]
 
 
