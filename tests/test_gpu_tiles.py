@@ -54,6 +54,8 @@ GROUPED = [
     ([40, 0, 3, 90], 96, 40, 1),                      # offset pointers
     ([200, 129, 64], 300, 136, 0),                    # K past 256, N past 128
     ([200, 129, 64, 0, 250], 320, 136, 0),            # whole 32-deep slices, N past 128
+    ([150, 0, 33, 131], 32, 8, 0),                     # one slice (it reloads itself), N = 8
+    ([257, 3, 128], 64, 260, 0),                       # two slices, three column tiles
 ]
 
 
