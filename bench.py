@@ -55,7 +55,8 @@ def parse(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--quick", action="store_true", help="headline only (no C3/C4/C5 extras, no CPU baseline)")
+    ap.add_argument("--quick", action="store_true",
+                    help="no CPU baseline and no extras unless --only names them (then without their CPU samples)")
     ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route,trace")
     ap.add_argument("--route-trace", default="", help="replay every frame of this .rrtrace file (extras.route_trace)")
     ap.add_argument("--profile", default="", choices=["", "headline", "c4", "c3", "c5"],
@@ -989,7 +990,7 @@ def main() -> int:
         roof["traffic"] = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
 
     extras = {}
-    if not args.quick:
+    if not args.quick or args.only:
         only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c4u", "c5", "route", "trace"}
         from raggedroute_amd import workloads
         if "c1" in only:

@@ -247,6 +247,26 @@ struct DmaLayout {
   __device__ static int swb(int k) { return 4 * ((k >> 2) & 3); }
 };
 
+// One 16-deep k chunk of a wave tile: MFMA step s (k = kk + 4g + s) of every
+// 16x16 tile before step s + 1 of any. Each accumulator still sums its steps
+// in ascending order, so the products are those of a tile-by-tile loop, but
+// consecutive MFMAs write different accumulators: a step never waits for the
+// result of the one issued just before it (a dependent MFMA on the same
+// accumulator issues about 12 cycles later than an independent one).
+template <int TM, int TN>
+__device__ __forceinline__ void mfma_steps(v4f (&acc)[TM][TN], const v4f (&af)[TM], const v4f (&bf)[TN]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // Tile space decode: row tiles are grouped kGroupM at a time so that workgroups
 // running together share both A row blocks and B column strips.
 __device__ __forceinline__ void decode_tile(int t, int row_tiles, int col_tiles, int* rt, int* ct) {
@@ -430,25 +450,16 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         const float* Bs = cur + S::BM * S::kLd;
 #pragma unroll
         for (int kk = 0; kk < S::BK; kk += 16) {
-          float4 af[TM], bf[TN];
+          v4f af[TM], bf[TN];
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
-            af[i] = *reinterpret_cast<const float4*>(As + (wm0 + i * 16 + li) * S::kLd + kk + 4 * g);
+            af[i] = *reinterpret_cast<const v4f*>(As + (wm0 + i * 16 + li) * S::kLd + kk + 4 * g);
           }
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
-            bf[j] = *reinterpret_cast<const float4*>(Bs + (wn0 + j * 16 + li) * S::kLd + kk + 4 * g);
+            bf[j] = *reinterpret_cast<const v4f*>(Bs + (wn0 + j * 16 + li) * S::kLd + kk + 4 * g);
           }
-#pragma unroll
-          for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
-            }
-          }
+          mfma_steps<TM, TN>(acc, af, bf);
         }
       };
       if constexpr (DMA) {
@@ -518,11 +529,11 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         // lets the compiler leave the reads after the loads unwaited)
         auto multiply_dma = [&](int kt, const float* __restrict__ As, float* __restrict__ next) {
           const float* Bs = As + D::kAFloats;
-          float4 af[2][TM];
-          float bf[2][TN][4];
+          v4f af[2][TM];
+          v4f bf[2][TN];
           auto read = [&](int h) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const float4*>(As + aoff[i][h]);
+            for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const v4f*>(As + aoff[i][h]);
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -535,18 +546,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
           issue(kt + 1 < nk ? kt + 1 : kt, next);
           read(1);
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-#pragma unroll
-              for (int j = 0; j < TN; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].x, bf[h][j][0], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].y, bf[h][j][1], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].z, bf[h][j][2], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[h][i].w, bf[h][j][3], acc[i][j], 0, 0, 0);
-              }
-            }
-          }
+          for (int h = 0; h < 2; ++h) mfma_steps<TM, TN>(acc, af[h], bf[h]);
           // Issue order: the first half's reads, then the next slice's loads
           // and the second half's reads spread over the first half's MFMAs.
           __builtin_amdgcn_sched_group_barrier(0x100, TM + 2 * TN, 0);  // LDS reads

@@ -170,6 +170,10 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
 
 struct StripRange {
   int s0, s1;
+  // Half strips [h0, h1) of the range (half strip 2 s: the left half of strip
+  // s's columns, 2 s + 1: the right half); strips s0 and s1 - 1 may be shared
+  // with the neighbouring workers, which own their other halves.
+  int h0, h1;
   // Segment-aligned ranges: all strips lie in segment e, whose strips start
   // at pre, rows at off, cnt rows (e = -1: the range may span segments).
   int e, pre, off, cnt;
@@ -189,40 +193,53 @@ __device__ __forceinline__ StripRange even_range(int total, int grid, int worker
   StripRange r;
   r.s0 = worker * q + (worker < rem ? worker : rem);
   r.s1 = r.s0 + q + (worker < rem ? 1 : 0);
+  r.h0 = 2 * r.s0;
+  r.h1 = 2 * r.s1;
   r.e = -1;
   r.pre = r.off = r.cnt = 0;
   return r;
 }
 
-// Strips [s0, s1) of one worker. Preferred: segment-aligned ranges, m strips
-// per worker with ceil(strips_e / m) workers per segment, so a worker loads
-// one segment's B once. m is the smallest of m_even = ceil(total / grid) and
-// m_even + 1 for which those workers fit the grid; otherwise (many small
-// segments), or when m exceeds cap, the even contiguous split is used.
+// Strips [s0, s1) of one worker. Preferred: segment-aligned ranges counted in
+// half strips (the left or right half of a strip's columns, computed by half
+// of the waves), m halves per worker with w_e = ceil(2 strips_e / m) workers
+// per segment, each taking an even share (at most m) of the segment's halves,
+// so a worker loads one segment's B once. m is the smallest of
+// m_even = ceil(2 total / grid) and m_even + 1 for which those workers fit
+// the grid; otherwise (many small segments), or when a worker's strips would
+// exceed cap, the even contiguous split of whole strips is used. (With 2.1
+// strips per worker on average, whole strips put 3 on some workers; halves
+// put at most 2 strips and one half strip, which runs half the MFMA work.)
+// U: units per strip, 2 (half strips) when a strip has two waves per SIMD
+// (eight waves: a half strip keeps every SIMD busy with one wave), else 1.
+template <int U>
 __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk, int segments,
                                                     int total, int grid, int worker, int cap) {
+  static_assert(U == 1 || U == 2, "whole or half strips");
   const int lane = lane_id();
-  const int m0 = total > 0 ? (total + grid - 1) / grid : 1;
+  const int m0 = total > 0 ? (U * total + grid - 1) / grid : U;
   const int m1 = m0 + 1;
   auto need = [&](int m) {
     int32_t n = 0;
 #pragma unroll
     for (int j = 0; j < kMaxBlocks; ++j) {
-      if (j < nblk) n += wave_sum(ceil_div32(strips_of(t.cnt[j]), m));
+      if (j < nblk) n += wave_sum(ceil_div32(U * strips_of(t.cnt[j]), m));
     }
     return n;
   };
-  const bool fit0 = m0 <= cap && need(m0) <= grid;
-  const bool fit1 = !fit0 && m1 <= cap && need(m1) <= grid;  // (only asked when m0 fails)
+  // m halves touch at most m / 2 + 1 strips (+1 when the range starts with a right half)
+  auto fits_cap = [&](int m) { return (U == 2 ? m / 2 + 1 : m) <= cap; };
+  const bool fit0 = fits_cap(m0) && need(m0) <= grid;
+  const bool fit1 = !fit0 && fits_cap(m1) && need(m1) <= grid;  // (only asked when m0 fails)
   if (!fit0 && !fit1) return even_range(total, grid, worker);
   const int m = fit0 ? m0 : m1;
-  // workers of segment e: [wpre_e, wpre_e + ceil(strips_e / m))
+  // workers of segment e: [wpre_e, wpre_e + ceil(2 strips_e / m))
   int32_t wpre[kMaxBlocks];
   int32_t carry = 0;
 #pragma unroll
   for (int j = 0; j < kMaxBlocks; ++j) {
     if (j < nblk) {
-      const int32_t wk = ceil_div32(strips_of(t.cnt[j]), m);
+      const int32_t wk = ceil_div32(U * strips_of(t.cnt[j]), m);
       const int32_t incl = rr::dev::wave_inclusive_scan(wk);
       wpre[j] = carry + incl - wk;
       carry += __builtin_amdgcn_readlane(incl, 63);
@@ -231,7 +248,7 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
     }
   }
   StripRange r;
-  r.s0 = r.s1 = 0;
+  r.s0 = r.s1 = r.h0 = r.h1 = 0;
   r.e = -1;
   r.pre = r.off = r.cnt = 0;
   if (worker < carry) {
@@ -247,10 +264,16 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
     const int first = seg_field(wpre, nblk, e);
     const int pre_e = seg_field(t.pre, nblk, e);
     const int cnt_e = seg_field(t.cnt, nblk, e);
-    const int end_e = pre_e + strips_of(cnt_e);
-    r.s0 = pre_e + (worker - first) * m;
-    r.s1 = r.s0 + m < end_e ? r.s0 + m : end_e;
-    if (r.s0 > r.s1) r.s0 = r.s1;
+    const int units = U * strips_of(cnt_e);
+    const int workers = ceil_div32(units, m);  // >= 1: worker lies in this segment
+    const int j = worker - first;
+    // even share: units [j H / w, (j + 1) H / w)
+    const int lo = static_cast<int>(static_cast<long long>(j) * units / workers) * (2 / U);
+    const int hi = static_cast<int>(static_cast<long long>(j + 1) * units / workers) * (2 / U);
+    r.h0 = 2 * pre_e + lo;
+    r.h1 = 2 * pre_e + hi;
+    r.s0 = pre_e + lo / 2;
+    r.s1 = pre_e + (hi + 1) / 2;
     r.e = e;
     r.pre = pre_e;
     r.off = seg_field(t.off, nblk, e);
@@ -478,11 +501,18 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   if constexpr (kSingle) {
     range = even_range(total, grid, worker);
   } else {
-    range = assign_strips(tab, nblk, E, total, grid, worker,
-                          MODE == kStripChain ? p.max_strips : INT_MAX);
+    range = assign_strips<kWaves == 8 ? 2 : 1>(tab, nblk, E, total, grid, worker,
+                                               MODE == kStripChain ? p.max_strips : INT_MAX);
   }
   const int s0 = range.s0;
   const int s1 = range.s1;
+  // Half strips: waves [0, kWaves / 2) compute the left half of a strip's
+  // columns, the others the right half. A wave runs strip s when its half is
+  // in [h0, h1); the worker with the left half writes the strip's route map
+  // and x_permuted rows (a shared strip's other worker only reads them).
+  const int side = wave >= kWaves / 2 ? 1 : 0;
+  auto runs = [&](int s) { return 2 * s + side >= range.h0 && 2 * s + side < range.h1; };
+  auto owns_map = [&](int s) { return 2 * s >= range.h0; };
   auto info = [&](int s) -> StripInfo {
     if constexpr (kSingle) {
       return StripInfo{0, s * kRows, p.M, s * kRows};
@@ -716,7 +746,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       // slot tid holds row (tid % 16) of strip s0 + tid / 16 (strip info tabulated above)
       const int row = s_info[4 * (tid / kRows) + 1] + tid % kRows;
       s_tok[tid] = route >= 0 ? token_of(route) : -1;
-      if (route >= 0) {
+      if (route >= 0 && owns_map(s0 + tid / kRows)) {
         p.route_pos[route] = row;
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
       }
@@ -741,7 +771,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       }
     }
     if constexpr (MODE == kStripChain) {
-      if (src >= 0 && p.x_permuted != nullptr) {  // gathered rows -> x_permuted
+      if (src >= 0 && p.x_permuted != nullptr && owns_map(s)) {  // gathered rows -> x_permuted
         float* out = p.x_permuted + static_cast<std::size_t>(si.row0 + a_row) * K;
 #pragma unroll
         for (int u = 0; u < kALoads; ++u) {
@@ -767,26 +797,35 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     // alternate, each keeping its own k order.
     v4f acc[kTiles];
     acc[0] = v4f{0.0F, 0.0F, 0.0F, 0.0F};
-    const float* aw = As + li * kLd + 4 * g;
-    // Software pipelined: chunk c + 1's A operands are read from LDS before
-    // chunk c's MFMAs issue, so their latency hides behind that chunk's
-    // dependent MFMA chain (k order unchanged). B comes from registers.
-    v4f af_next = *reinterpret_cast<const v4f*>(aw);
+    const bool active = runs(s);  // (wave-uniform)
+    if (active) {
+      const float* aw = As + li * kLd + 4 * g;
+      // Software pipelined: chunk c + 1's A operands are read from LDS before
+      // chunk c's MFMAs issue, so their latency hides behind that chunk's
+      // dependent MFMA chain (k order unchanged). B comes from registers.
+      v4f af_next = *reinterpret_cast<const v4f*>(aw);
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
-      if (c < chunks) {
-        const v4f af = af_next;
-        if (c + 1 < chunks) af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
-        // (the scheduler would otherwise sink that read to its use)
-        __builtin_amdgcn_sched_barrier(0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bq[c][0], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bq[c][1], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bq[c][2], acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bq[c][3], acc[0], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int c = 0; c < kMaxChunks; ++c) {
+        if (c < chunks) {
+          const v4f af = af_next;
+          if (c + 1 < chunks) af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
+          // (the scheduler would otherwise sink that read to its use)
+          __builtin_amdgcn_sched_barrier(0);
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bq[c][0], acc[0], 0, 0, 0);
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bq[c][1], acc[0], 0, 0, 0);
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bq[c][2], acc[0], 0, 0, 0);
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bq[c][3], acc[0], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (kDeferred) {
+          if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
+        }
       }
-      if constexpr (kDeferred) {
-        if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
+    } else if constexpr (kDeferred) {
+      // the other half's strip: only the previous strip's epilogue
+      if (pending) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) epilogue_row(r, acc_prev, prev);
       }
     }
     if (s + 1 < s1 && cur.e != si.e) load_b(cur.e);  // the next strip's segment
@@ -804,7 +843,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
           ep_w[r] = s_w[prev.rank0 + 4 * g + r];
         }
       }
-      pending = true;
+      pending = active;
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) epilogue_row(r, acc, si);
