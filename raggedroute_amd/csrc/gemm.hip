@@ -210,7 +210,7 @@ struct Stage {
       if (xrow[p] == nullptr) continue;
       float* ptr = xrow[p] + k0;
       if (VEC) {
-        if (k < K) *reinterpret_cast<float4*>(ptr) = make_float4(a[p][0], a[p][1], a[p][2], a[p][3]);
+        if (k < K) __builtin_nontemporal_store(v4f{a[p][0], a[p][1], a[p][2], a[p][3]}, reinterpret_cast<v4f*>(ptr));
       } else if (k + 3 < K) {
         *reinterpret_cast<f4u*>(ptr) = f4u{a[p][0], a[p][1], a[p][2], a[p][3]};
       } else {
@@ -569,9 +569,9 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
             const int r = f >> 3;
             if (r < rows) {
               const int kc = (f & 7) ^ D::swa(r);
-              const float4 v = *reinterpret_cast<const float4*>(As + 4 * f);
-              *reinterpret_cast<float4*>(prm.x_permuted + static_cast<std::size_t>(row0 + r) * K +
-                                         kt * D::kBK + 4 * kc) = v;
+              const v4f v = *reinterpret_cast<const v4f*>(As + 4 * f);
+              __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(prm.x_permuted + static_cast<std::size_t>(row0 + r) * K +
+                                                                   kt * D::kBK + 4 * kc));
             }
           }
         };
@@ -672,7 +672,12 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
           for (int j = 0; j < TN; ++j) {
             const int col = n0 + wn0 + j * 16 + li;
             if (col < N) {
-              yrow[col] = acc[i][j][r];
+              if (comb != nullptr) {
+                // combined: y_permuted is not read again by the chain
+                __builtin_nontemporal_store(acc[i][j][r], yrow + col);
+              } else {
+                yrow[col] = acc[i][j][r];
+              }
               if constexpr (MODE == kChainGrouped) {
                 // Both routes of a token add into the zeroed output: fl(0 + a) + b
                 // is the same in either order, so the combine is deterministic

@@ -550,6 +550,13 @@ __host__ __device__ inline uint32_t quads_of(int width) { return (static_cast<ui
 // in token-major order, grid-stride. A wave per token would leave most lanes
 // idle here (the 128-float rows of the headline unpermute ran at 6.4 us that
 // way, 4.0 us with items).
+// KMAX > 0 (top_k <= KMAX): a token's route positions (and weights) are all
+// loaded before any is used, reloading route top_k - 1 in the slots past
+// top_k, so a token costs one round trip for its positions and one for its
+// rows instead of one per route. KMAX = 0: any top_k, one route at a time.
+// Whole quads are written with nontemporal stores, as in the wide-row kernels
+// (headline permute stage 8.0 -> 7.5 us).
+template <int KMAX>
 __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __restrict__ x,
                                                               const int32_t* __restrict__ route_pos,
                                                               float* __restrict__ x_permuted,
@@ -563,18 +570,31 @@ __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __res
     const uint32_t c = i - t * cols;
     const int k0 = static_cast<int>(4 * c);
     const float* src = x + static_cast<std::size_t>(t) * hidden + k0;
+    const std::size_t base = static_cast<std::size_t>(t) * top_k;
     if (k0 + 4 <= hidden) {
       const f4u v = *reinterpret_cast<const f4u*>(src);
-      for (int j = 0; j < top_k; ++j) {
-        const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
-        if (pos >= 0 && pos < routes) {
-          *reinterpret_cast<f4u*>(x_permuted + static_cast<std::size_t>(pos) * hidden + k0) = v;
+      if constexpr (KMAX > 0) {
+        int32_t pos[KMAX];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) pos[j] = route_pos[base + (j < top_k ? j : top_k - 1)];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+          if (j < top_k && pos[j] >= 0 && pos[j] < routes) {
+            __builtin_nontemporal_store(v, reinterpret_cast<f4u*>(x_permuted + static_cast<std::size_t>(pos[j]) * hidden + k0));
+          }
+        }
+      } else {
+        for (int j = 0; j < top_k; ++j) {
+          const int32_t pos = route_pos[base + j];
+          if (pos >= 0 && pos < routes) {
+            *reinterpret_cast<f4u*>(x_permuted + static_cast<std::size_t>(pos) * hidden + k0) = v;
+          }
         }
       }
     } else {
       const int n = hidden - k0;  // 1..3
       for (int j = 0; j < top_k; ++j) {
-        const int32_t pos = route_pos[static_cast<std::size_t>(t) * top_k + j];
+        const int32_t pos = route_pos[base + j];
         if (pos >= 0 && pos < routes) {
           float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden + k0;
           for (int q = 0; q < n; ++q) dst[q] = src[q];
@@ -584,6 +604,14 @@ __global__ __launch_bounds__(256) void rr_permute_copy_kernel(const float* __res
   }
 }
 
+// Narrow rows, rank-order sum acc = fl(acc + fl(w * v)) over the token's
+// valid routes. KMAX > 0 (top_k <= KMAX): positions and weights of every
+// route, then every route's quad (an invalid position reads row 0 and is
+// left out of the sum), then the sum in rank order: two round trips per token
+// instead of two per route (post-route chain T512 top_k 8 19.6 -> 16.6 us).
+// KMAX = 0: any top_k, one route at a time. Whole quads of y leave with
+// nontemporal stores.
+template <int KMAX>
 __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restrict__ y_permuted,
                                                            const int32_t* __restrict__ route_pos,
                                                            const float* __restrict__ route_weights,
@@ -598,25 +626,57 @@ __global__ __launch_bounds__(256) void rr_unpermute_kernel(const float* __restri
     const uint32_t c = i - t * cols;
     const int k0 = static_cast<int>(4 * c);
     float* out = y + static_cast<std::size_t>(t) * output + k0;
+    const std::size_t base = static_cast<std::size_t>(t) * top_k;
     if (k0 + 4 <= output) {
       f4u acc = f4u{0.0F, 0.0F, 0.0F, 0.0F};
-      for (int j = 0; j < top_k; ++j) {
-        const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
-        const int32_t pos = route_pos[route];
-        if (pos < 0 || pos >= routes) continue;
-        const float w = route_weights[route];
-        const f4u v = *reinterpret_cast<const f4u*>(y_permuted + static_cast<std::size_t>(pos) * output + k0);
-        acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
-        acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
-        acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
-        acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
+      if constexpr (KMAX > 0) {
+        int32_t pos[KMAX];
+        float w[KMAX];
+        f4u v[KMAX];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+          const std::size_t route = base + (j < top_k ? j : top_k - 1);
+          pos[j] = route_pos[route];
+          w[j] = route_weights[route];
+        }
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+          const bool ok = pos[j] >= 0 && pos[j] < routes;
+          v[j] = *reinterpret_cast<const f4u*>(y_permuted + static_cast<std::size_t>(ok ? pos[j] : 0) * output + k0);
+        }
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+          if (j < top_k) {
+            const bool ok = pos[j] >= 0 && pos[j] < routes;
+            const float sx = __fadd_rn(acc.x, __fmul_rn(w[j], v[j].x));
+            const float sy = __fadd_rn(acc.y, __fmul_rn(w[j], v[j].y));
+            const float sz = __fadd_rn(acc.z, __fmul_rn(w[j], v[j].z));
+            const float sw = __fadd_rn(acc.w, __fmul_rn(w[j], v[j].w));
+            acc.x = ok ? sx : acc.x;
+            acc.y = ok ? sy : acc.y;
+            acc.z = ok ? sz : acc.z;
+            acc.w = ok ? sw : acc.w;
+          }
+        }
+      } else {
+        for (int j = 0; j < top_k; ++j) {
+          const std::size_t route = base + j;
+          const int32_t pos = route_pos[route];
+          if (pos < 0 || pos >= routes) continue;
+          const float w = route_weights[route];
+          const f4u v = *reinterpret_cast<const f4u*>(y_permuted + static_cast<std::size_t>(pos) * output + k0);
+          acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
+          acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
+          acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
+          acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
+        }
       }
-      *reinterpret_cast<f4u*>(out) = acc;
+      __builtin_nontemporal_store(acc, reinterpret_cast<f4u*>(out));
     } else {
       const int n = output - k0;  // 1..3
       float acc[3] = {0.0F, 0.0F, 0.0F};
       for (int j = 0; j < top_k; ++j) {
-        const std::size_t route = static_cast<std::size_t>(t) * top_k + j;
+        const std::size_t route = base + j;
         const int32_t pos = route_pos[route];
         if (pos < 0 || pos >= routes) continue;
         const float w = route_weights[route];
@@ -986,8 +1046,16 @@ hipError_t launch_permute_copy(const float* x, const int32_t* route_pos, float* 
   } else {
     const uint64_t items = static_cast<uint64_t>(tokens) * quads_of(hidden);
     if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;  // 32-bit item indices
-    rr_permute_copy_kernel<<<stream_grid(items), 256, 0, stream>>>(x, route_pos, x_permuted, tokens,
-                                                                   top_k, hidden, routes);
+    const unsigned grid = stream_grid(items);
+    if (top_k <= 2) {
+      rr_permute_copy_kernel<2><<<grid, 256, 0, stream>>>(x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+    } else if (top_k <= 4) {
+      rr_permute_copy_kernel<4><<<grid, 256, 0, stream>>>(x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+    } else if (top_k <= 8) {
+      rr_permute_copy_kernel<8><<<grid, 256, 0, stream>>>(x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+    } else {
+      rr_permute_copy_kernel<0><<<grid, 256, 0, stream>>>(x, route_pos, x_permuted, tokens, top_k, hidden, routes);
+    }
   }
   return hipGetLastError();
 }
@@ -1128,8 +1196,16 @@ hipError_t unpermute_gather(const float* y_permuted, const int32_t* route_pos,
   } else {
     const uint64_t items = static_cast<uint64_t>(tokens) * quads_of(output);
     if (items >= (uint64_t{1} << 32)) return hipErrorInvalidValue;  // 32-bit item indices
-    rr_unpermute_kernel<<<stream_grid(items), 256, 0, stream>>>(y_permuted, route_pos, route_weights,
-                                                                y, tokens, top_k, output);
+    const unsigned grid = stream_grid(items);
+    if (top_k <= 2) {
+      rr_unpermute_kernel<2><<<grid, 256, 0, stream>>>(y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+    } else if (top_k <= 4) {
+      rr_unpermute_kernel<4><<<grid, 256, 0, stream>>>(y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+    } else if (top_k <= 8) {
+      rr_unpermute_kernel<8><<<grid, 256, 0, stream>>>(y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+    } else {
+      rr_unpermute_kernel<0><<<grid, 256, 0, stream>>>(y_permuted, route_pos, route_weights, y, tokens, top_k, output);
+    }
   }
   return hipGetLastError();
 }

@@ -691,7 +691,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) {
           const int col = col0 + 16 * t;
-          if (col < N) crow[col] = a[t][r];
+          if (col < N) {
+            // a combined chain never reads y_permuted again: nontemporal
+            // stores leave no dirty lines for the end-of-launch write-back
+            if (p.combine) {
+              __builtin_nontemporal_store(a[t][r], crow + col);
+            } else {
+              crow[col] = a[t][r];
+            }
+          }
         }
         if (p.combine) {
           // Both routes of a token add into the zeroed output: fl(0 + a) + b
@@ -712,7 +720,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) {
           const int col = col0 + 16 * t;
-          if (col < N) crow[col] = a[t][r];
+          if (col < N) {
+            if constexpr (MODE == kStripRouterGate) {
+              __builtin_nontemporal_store(a[t][r], crow + col);  // (the gate reads LDS)
+            } else {
+              crow[col] = a[t][r];
+            }
+          }
         }
       }
     }
@@ -776,7 +790,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
 #pragma unroll
         for (int u = 0; u < kALoads; ++u) {
           const int k = 4 * (a_col + kRowThreads * u);
-          if (k < K) *reinterpret_cast<v4f*>(out + k) = a_regs[u];
+          if (k < K) __builtin_nontemporal_store(a_regs[u], reinterpret_cast<v4f*>(out + k));
         }
       }
       if (s == s0 && tid < (s1 - s0) * kRows) s_w[tid] = w_pending;
