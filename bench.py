@@ -782,17 +782,19 @@ def profile(torch, device, case):
     if case == "headline":
         cfg = workloads.HEADLINE
         ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
-        for _ in range(5):
+        # (enough back-to-back calls for the clocks to settle: the later
+        # dispatches of each kernel are the steady state)
+        for _ in range(50):
             ch.chain()
         torch.cuda.synchronize()
         for index in range(len(ch.rr.chain_fused_launch_names(ch.chain_args, cfg.from_tokens))):
-            for _ in range(3):
+            for _ in range(20):
                 ch.fused_launch(index)
         for name in ch.stage_args:
-            for _ in range(3):
+            for _ in range(20):
                 ch.stage(name)
         torch.cuda.synchronize()
-        print("profile: headline done (5 chains, 3 x each fused launch, 3 x each stage)", flush=True)
+        print("profile: headline done (50 chains, 20 x each fused launch, 20 x each stage)", flush=True)
     elif case == "c4":
         c4(torch, device, reps=2, samples=3)
         print("profile: c4 done", flush=True)
@@ -802,14 +804,15 @@ def profile(torch, device, case):
     elif case == "c5":
         cfg = workloads.C5
         ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
-        # Back to back with no host wait between calls, so that the calls
-        # after the first few run at the clocks of the timed bench loops.
-        for _ in range(10):
+        # Back to back with no host wait between calls: the expert GEMM needs
+        # about 20 calls before its clock settles, so the last 10 of 30 are
+        # the steady state of the timed bench loops.
+        for _ in range(30):
             ch.chain()
-        for _ in range(10):
+        for _ in range(30):
             ch.stage("grouped_gemm")
         torch.cuda.synchronize()
-        print("profile: c5 done (10 chains, 10 x grouped_gemm)", flush=True)
+        print("profile: c5 done (30 chains, 30 x grouped_gemm)", flush=True)
 
 
 # ------------------------------------------------------------ runner mode
