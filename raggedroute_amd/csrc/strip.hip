@@ -11,7 +11,9 @@
 //     64 floats), loaded straight from global memory (one load instruction
 //     reads 64 contiguous bytes of four k rows). B needs no LDS stage, no
 //     transposing stores and no barrier, and the first strip's MFMAs wait for
-//     each k chunk of B as it arrives rather than for all of it.
+//     each k chunk of B as it arrives rather than for all of it. The router
+//     (K = 256, four waves) instead keeps B in LDS, each wave filling its own
+//     columns with 16 direct loads.
 //   A rows (16 x K) are loaded by the whole workgroup with row-contiguous
 //     float4 accesses into registers, stored to one of two [16][K + 4] LDS
 //     stages (strips alternate, one barrier per strip), and the next strip's
@@ -104,6 +106,17 @@ __device__ __forceinline__ v4f load_raw(const float* ptr) {
 
 __device__ __forceinline__ v4f zero_unless(bool valid, const v4f& v) {
   return valid ? v : v4f{0.0F, 0.0F, 0.0F, 0.0F};
+}
+
+// s_waitcnt vmcnt(n) for n known after unrolling (the builtin takes a constant)
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+#define RR_VM(i) case i: __builtin_amdgcn_s_waitcnt(0x0F70 | i); break;
+    RR_VM(0) RR_VM(1) RR_VM(2) RR_VM(3) RR_VM(4) RR_VM(5) RR_VM(6) RR_VM(7)
+    RR_VM(8) RR_VM(9) RR_VM(10) RR_VM(11) RR_VM(12) RR_VM(13) RR_VM(14) RR_VM(15)
+#undef RR_VM
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
 }
 
 // Per-lane segment table: lane l holds segment e = 64 j + l (segments <= 256)
@@ -337,6 +350,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   float* s_lg = As2 + 2 * kRows * kLd;  // router: [16][kLgLd] logits of the strip
   // chain: [waves][kMaxSegs][4] segment lists (16-byte aligned)
   int32_t* s_seglist = reinterpret_cast<int32_t*>(s_lg + (MODE == kStripRouterGate ? kRows * kLgLd : 0));
+  // Router with K = 256 and four waves: B lives in LDS, each wave's 16 columns
+  // in 16 blocks of 1 KiB (one per k chunk) filled by the wave's own direct
+  // loads (global_load_lds_dwordx4, lane L -> bytes [16 L, 16 L + 16) of the
+  // block). Lane L fetches row 4 ((L >> 2) & 3) + (L >> 4) of the chunk and
+  // columns 4 (L & 3) .. + 3, so the MFMA operand of lane (li, g) at step s,
+  // B[16 c + 4 g + s][16 w + li], sits at float 64 s + 16 g + li of block c:
+  // the 64 lanes of a read hit 64 distinct banks, and steps s, s + 1 pair into
+  // one ds_read2st64_b32. No cross-wave dependency: no barrier for B.
+  constexpr bool kBLds = MODE == kStripRouterGate && CHUNKS == kMaxChunks && WAVES == 4;
+  float* s_bl = s_lg + kRows * kLgLd;  // router (kBLds): [waves][16][256]
   int32_t* s_slot = s_seglist + (MODE == kStripChain ? kWaves * kMaxSegs * 4 : 0);  // chain: [max_strips * 16]
   float* s_w = reinterpret_cast<float*>(s_slot + (MODE == kStripChain ? p.max_strips * kRows : 0));
   // chain: [max_strips * 16] token of each slot's route (-1: none), [max_strips][4] strip info
@@ -361,8 +384,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // contiguous bytes of one k row, a load instruction four rows. Columns past
   // N read column N - 1 (their outputs are never stored); rows past K are
   // zero (lanes masked off the load keep the zero: no wait for the data).
-  float bq[kMaxChunks][4];
+  float bq[kBLds ? 1 : kMaxChunks][4];
   auto load_b = [&](int e, int c_lo = 0, int c_hi = kMaxChunks) {
+    if constexpr (kBLds) {
+      (void)e; (void)c_lo; (void)c_hi;
+      const int r = 4 * ((lane >> 2) & 3) + (lane >> 4);
+      const int n = 16 * wave + 4 * (lane & 3);
+      const float* src = p.W + r * N + (n < N ? n : N - 4);  // (N % 4 == 0)
+      float* dst = s_bl + wave * (kMaxChunks * 256);
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        __builtin_amdgcn_global_load_lds(src + 16 * c * N, dst + 256 * c, 16, 0, 0);
+      }
+      return;
+    }
     const float* W = p.W + static_cast<std::size_t>(e) * K * N;
     const int n = 16 * wave + li;
     const int nc = n < N ? n : N - 1;
@@ -818,6 +853,43 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       // chunk c's MFMAs issue, so their latency hides behind that chunk's
       // dependent MFMA chain (k order unchanged). B comes from registers.
       v4f af_next = *reinterpret_cast<const v4f*>(aw);
+      if constexpr (kBLds) {
+        // B chunk c from LDS once the wave's direct load of block c is done:
+        // vmcnt(15 - c) (later memory operations only make the wait longer).
+        // (The compiler already waits for every direct load before the A
+        // stage's LDS store, which it cannot prove disjoint from them; issuing
+        // B this way still beats 64 register loads per lane, which pass the
+        // 63 a wave may have outstanding: router launch 5.05 -> 4.77 us.)
+        auto run = [&](const float* __restrict__ bl) {
+          v4f bf_next;
+          __builtin_amdgcn_s_waitcnt(0x0F70 | 15);
+          bf_next[0] = bl[li + 16 * g];
+          bf_next[1] = bl[li + 16 * g + 64];
+          bf_next[2] = bl[li + 16 * g + 128];
+          bf_next[3] = bl[li + 16 * g + 192];
+#pragma unroll
+          for (int c = 0; c < kMaxChunks; ++c) {
+            const v4f af = af_next;
+            const v4f bf = bf_next;
+            if (c + 1 < kMaxChunks) {
+              af_next = *reinterpret_cast<const v4f*>(aw + 16 * (c + 1));
+              wait_vmcnt(14 - c);
+              const float* bc = bl + 256 * (c + 1) + li + 16 * g;
+              bf_next[0] = bc[0];
+              bf_next[1] = bc[64];
+              bf_next[2] = bc[128];
+              bf_next[3] = bc[192];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf[0], acc[0], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf[1], acc[0], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf[2], acc[0], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf[3], acc[0], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        };
+        run(s_bl + wave * (kMaxChunks * 256));
+      } else {
 #pragma unroll
       for (int c = 0; c < kMaxChunks; ++c) {
         if (c < chunks) {
@@ -834,6 +906,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if constexpr (kDeferred) {
           if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
         }
+      }
       }
     } else if constexpr (kDeferred) {
       // the other half's strip: only the previous strip's epilogue
@@ -953,6 +1026,9 @@ std::size_t strip_lds(int bn, int mode, int K, int segments, int max_strips) {
   std::size_t bytes = stage * sizeof(float);
   const int waves = strip_waves(bn, mode);
   if (mode == kStripRouterGate) bytes += static_cast<std::size_t>(kRows) * (bn + 4) * sizeof(float);
+  if (mode == kStripRouterGate && K == 256 && waves == 4) {
+    bytes += static_cast<std::size_t>(waves) * kMaxChunks * 256 * sizeof(float);  // B in LDS
+  }
   if (mode == kStripChain) {
     bytes += static_cast<std::size_t>(waves) * kMaxSegs * 4 * sizeof(int32_t);  // segment lists
     bytes += 3 * static_cast<std::size_t>(max_strips) * kRows * sizeof(int32_t);  // slots, weights, tokens
