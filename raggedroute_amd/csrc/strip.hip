@@ -401,15 +401,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     const float* W = p.W + static_cast<std::size_t>(e) * K * N;
     const int n = 16 * wave + li;
     const int nc = n < N ? n : N - 1;
+    // K = 16 CHUNKS exactly: the lane's column at row 4g, each load adding a
+    // wave-uniform row offset (one pointer per lane; with per-load lane
+    // offsets the compiler keeps 64 addresses live and the chain launch
+    // sits at the 256-register limit)
+    const float* Wl = W + 4 * g * N + nc;
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
       if (c < chunks && c >= c_lo && c < c_hi) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int k = 16 * c + 4 * g + s;  // (k * N < 2^31: K <= 256, N <= 128)
           if constexpr (CHUNKS > 0) {
-            bq[c][s] = W[k * N + nc];  // K = 16 CHUNKS exactly
+            bq[c][s] = Wl[(16 * c + s) * N];
           } else {
+            const int k = 16 * c + 4 * g + s;  // (k * N < 2^31: K <= 256, N <= 128)
             float v = 0.0F;
             if (k < K) v = W[k * N + nc];
             bq[c][s] = v;
@@ -1057,8 +1062,9 @@ hipError_t launch_strip_3(const StripParams& p, int grid, std::size_t lds, hipSt
 
 template <int BN, int MODE>
 hipError_t launch_strip_2(const StripParams& p, int grid, std::size_t lds, hipStream_t stream) {
-  return p.K == 256 ? launch_strip_3<BN, MODE, 16>(p, grid, lds, stream)
-                    : launch_strip_3<BN, MODE, 0>(p, grid, lds, stream);
+  if (p.K == 256) return launch_strip_3<BN, MODE, 16>(p, grid, lds, stream);
+  if (p.K == 128) return launch_strip_3<BN, MODE, 8>(p, grid, lds, stream);
+  return launch_strip_3<BN, MODE, 0>(p, grid, lds, stream);
 }
 
 template <int MODE>
