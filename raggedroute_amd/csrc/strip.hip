@@ -385,6 +385,26 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // N read column N - 1 (their outputs are never stored); rows past K are
   // zero (lanes masked off the load keep the zero: no wait for the data).
   float bq[kBLds ? 1 : kMaxChunks][4];
+  // chain at K = 256: the B of a later segment of the range, loaded ahead
+  // (at K = 128 a segment's B arrives soon enough and the early loads cost:
+  // post-route chains at the release shapes +0.1-0.4 us)
+  constexpr bool kPfB = MODE == kStripChain && CHUNKS == kMaxChunks && !kBLds;
+  float bq2[kPfB ? kMaxChunks : 1][4];
+  int pf_e = -1;  // segment held in bq2 (-1: none)
+  auto load_b2 = [&](int e) {
+    if constexpr (kPfB) {
+      const int n = 16 * wave + li;
+      const int nc = n < N ? n : N - 1;
+      const float* Wl = p.W + static_cast<std::size_t>(e) * K * N + 4 * g * N + nc;
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bq2[c][r] = Wl[(16 * c + r) * N];
+      }
+    } else {
+      (void)e;
+    }
+  };
   auto load_b = [&](int e, int c_lo = 0, int c_hi = kMaxChunks) {
     if constexpr (kBLds) {
       (void)e; (void)c_lo; (void)c_hi;
@@ -920,7 +940,30 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         for (int r = 0; r < 4; ++r) epilogue_row(r, acc_prev, prev);
       }
     }
-    if (s + 1 < s1 && cur.e != si.e) load_b(cur.e);  // the next strip's segment
+    if (s + 1 < s1 && cur.e != si.e) {  // the next strip's segment
+      if (kPfB && pf_e == cur.e) {
+#pragma unroll
+        for (int c = 0; c < kMaxChunks; ++c) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bq[c][r] = bq2[c][r];
+        }
+        pf_e = -1;
+      } else {
+        load_b(cur.e);
+      }
+    } else if constexpr (kPfB) {
+      // A range whose last segment starts after its second strip: that
+      // segment's B is loaded now, behind the first strip's MFMAs, into a
+      // second register set (instead of after the MFMAs of the strip before
+      // the switch, where the next strip's MFMAs would wait for it)
+      if (s == s0 && s1 - s0 >= 3) {
+        const int e_last = __builtin_amdgcn_readfirstlane(s_info[4 * (s1 - 1 - s0)]);
+        if (e_last != si.e) {
+          load_b2(e_last);
+          pf_e = e_last;
+        }
+      }
+    }
     if constexpr (kDeferred) {
       // (rows 0..3 of the previous strip went out at c = 3, 7, 11, 15: the
       // calls sit outside the c < chunks test, so short K emits them too)
