@@ -245,6 +245,9 @@ def run_stages(cfg, inp, device, ctx):
     # K tails of the strip kernel's register B: 16 chunks with masked rows
     # (B issued after the route map), 14 chunks (before it)
     ("tokens", 700, 64, 252, 128), ("logits", 900, 32, 224, 96),
+    # K = 256 with two-strip segments: workgroup ranges span up to three
+    # segments (a later segment's B loaded ahead, the middle one on the switch)
+    ("tokens", 4096, 256, 256, 128), ("tokens", 2048, 256, 256, 64),
 ])
 @pytest.mark.parametrize("with_inverse", [True, False])
 def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):
