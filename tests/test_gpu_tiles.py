@@ -56,6 +56,8 @@ GROUPED = [
     ([200, 129, 64, 0, 250], 320, 136, 0),            # whole 32-deep slices, N past 128
     ([150, 0, 33, 131], 32, 8, 0),                     # one slice (it reloads itself), N = 8
     ([257, 3, 128], 64, 260, 0),                       # two slices, three column tiles
+    ([0, 300, 5, 1000, 0, 0, 77, 1], 128, 128, 0),  # strip K = 128 instance (8 chunks)
+    ([0, 300, 5, 1000, 0, 0, 77, 1], 128, 64, 1),   # ... four-wave strips, offset pointers
 ]
 
 
@@ -77,7 +79,7 @@ def test_grouped_tiles_bit_identical(ctx, device, tile_env, counts, k, n, offset
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 64, 256), (300, 128, 96), (500, 128, 244), (77, 40, 260),
-                                   (129, 17, 33)])
+                                   (129, 17, 33), (4096, 64, 128), (700, 128, 128)])
 def test_dense_tiles_bit_identical(ctx, device, tile_env, m, n, k):
     import torch
     from conftest import to_dev, to_host
