@@ -105,27 +105,27 @@ template <class S, bool VEC>
 struct Stage {
   float a[S::kALoads][4];
   float b[S::kBLoads][4];
-  // A slot p: its row's element at the slot's column; slots without a row
-  // point at row 0 (a valid address, never read: row_ok is false).
-  const float* arow[S::kALoads];
-  bool row_ok[S::kALoads];
-  float* xrow[S::kALoads];  // chain: the same element of the x_permuted row (nullptr: none)
+  // A slot p reads row src[p] of A (-1: no row; the slot loads zeros). The
+  // slots keep row indices, not pointers: per-slot 64-bit addresses of both
+  // prefetch stages pushed the 128 x 128 register-staged tile past 256 VGPRs.
+  int src[S::kALoads];
+  const float* a_base;
+  float* xp_base;  // chain: x_permuted (nullptr: not written)
+  int xp_row0;     // x_permuted row of the tile's first row
 
   // Once per tile: the thread's A slots (and x_permuted rows, when given).
   __device__ __forceinline__ void set_rows(const float* __restrict__ A, const int32_t* src_rows,
                                            int row0, int row_end, int K, float* x_permuted,
                                            int tid) {
+    (void)K;
+    a_base = A;
+    xp_base = x_permuted;
+    xp_row0 = row0;
 #pragma unroll
     for (int p = 0; p < S::kALoads; ++p) {
       const int f = tid + p * S::kThreads;
       const int r = f / (S::BK / 4);  // BK / 4 float4 per row
-      const int c = (f % (S::BK / 4)) * 4;
-      const int src = src_rows != nullptr ? src_rows[r] : (row0 + r < row_end ? row0 + r : -1);
-      row_ok[p] = src >= 0;
-      arow[p] = A + static_cast<std::size_t>(src >= 0 ? src : 0) * K + c;
-      xrow[p] = src >= 0 && x_permuted != nullptr
-                    ? x_permuted + static_cast<std::size_t>(row0 + r) * K + c
-                    : nullptr;
+      src[p] = src_rows != nullptr ? src_rows[r] : (row0 + r < row_end ? row0 + r : -1);
     }
   }
 
@@ -136,8 +136,8 @@ struct Stage {
       const int f = tid + p * S::kThreads;
       const int c = (f % (S::BK / 4)) * 4;
       const int k = k0 + c;
-      const bool has_row = row_ok[p];
-      const float* ptr = arow[p] + k0;
+      const bool has_row = src[p] >= 0;
+      const float* ptr = a_base + static_cast<std::size_t>(has_row ? src[p] : 0) * K + k;
       if (VEC) {
         if (has_row && k < K) {
           const float4 v = *reinterpret_cast<const float4*>(ptr);
@@ -207,8 +207,8 @@ struct Stage {
       const int f = tid + p * S::kThreads;
       const int c = (f % (S::BK / 4)) * 4;
       const int k = k0 + c;
-      if (xrow[p] == nullptr) continue;
-      float* ptr = xrow[p] + k0;
+      if (xp_base == nullptr || src[p] < 0) continue;
+      float* ptr = xp_base + static_cast<std::size_t>(xp_row0 + f / (S::BK / 4)) * K + k;
       if (VEC) {
         if (k < K) __builtin_nontemporal_store(v4f{a[p][0], a[p][1], a[p][2], a[p][3]}, reinterpret_cast<v4f*>(ptr));
       } else if (k + 3 < K) {
