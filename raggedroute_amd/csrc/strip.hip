@@ -586,13 +586,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   };
   StripInfo cur{};
   if (s0 < s1) cur = info(s0);
+  constexpr int kEarlyB = 12;  // chain: k chunks of B issued before the ranks
   if constexpr (MODE == kStripChain) {
-    // The first half of B (k chunks 0..7, 32 loads per lane) as soon as the
-    // first segment is known: it arrives while the ranks are computed. All of
-    // B here would reach the wave's limit of outstanding loads (63) and stall
-    // the rank passes at issue (measured at the headline shape: expert launch
-    // 19.6 us with all of B here, 18.5 us with half, 18.7 us with none).
-    if (s0 < s1) load_b(cur.e, 0, 8);
+    // k chunks 0..11 of B (48 loads per lane) as soon as the first segment is
+    // known: they arrive while the ranks are computed. All of B here would
+    // reach the wave's limit of outstanding loads (63) and stall the rank
+    // passes at issue (measured at the headline shape: expert launch 19.6 us
+    // with all of B here, 18.5 us with half, 18.7 us with none; with one
+    // pointer per lane for B, chunks 0..11 15.87 us against 16.13 us for
+    // 0..7, 16.12 for 0..9 and 15.98 for 0..13).
+    if (s0 < s1) load_b(cur.e, 0, kEarlyB);
   }
   if constexpr (MODE == kStripChain) {
     // Every strip's info, once and in parallel (wave w: strips s0 + w,
@@ -800,10 +803,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   StripInfo prev{};
   bool pending = false;
 
-  // Issue order (chain): the first half of B (above), the first strip's A
+  // Issue order (chain): k chunks 0..11 of B (above), the first strip's A
   // rows, the route map's weight loads and stores, then the rest of B.
   // Memory operations complete in order, so the A stage waits for the first
-  // half of B, A and the weights, and the first strip's MFMAs wait for the
+  // chunks of B, A and the weights, and the first strip's MFMAs wait for the
   // rest of B one k chunk at a time. Other modes: A rows, then all of B.
   int src = -1;
   if (s0 < s1) {
@@ -825,7 +828,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if (p.sorted_route != nullptr) p.sorted_route[row] = route;
       }
     }
-    if (s0 < s1) load_b(cur.e, 8, kMaxChunks);  // the rest of B
+    if (s0 < s1) load_b(cur.e, kEarlyB, kMaxChunks);  // the rest of B
   } else {
     if (s0 < s1) load_b(cur.e);
   }
