@@ -54,7 +54,8 @@ def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed calls before timing (default 20; runner mode: 5, the reference runner's)")
     ap.add_argument("--quick", action="store_true",
                     help="no CPU baseline and no extras unless --only names them (then without their CPU samples)")
     ap.add_argument("--only", default="", help="comma list of extras to run: c1,c2,c3,c4,c4u,c5,route,trace")
@@ -70,9 +71,11 @@ def parse(argv=None):
                          "(one or more pairs per flag, the flag repeatable)")
     ap.add_argument("--variant", default="auto", choices=["auto", "naive", "optimized"])
     ap.add_argument("--cache-mode", default="warm", choices=["warm", "cold_scrub"])
-    ap.add_argument("--cache-scrub-bytes", type=int, default=512 << 20)
-    ap.add_argument("--samples", type=int, default=20)
-    ap.add_argument("--kernel-repeats", type=int, default=10)
+    ap.add_argument("--cache-scrub-bytes", type=int, default=512 << 20,
+                    help="runner mode, cold_scrub: bytes written before every warmup call and sample")
+    ap.add_argument("--samples", type=int, default=10, help="runner mode: timed samples")
+    ap.add_argument("--kernel-repeats", type=int, default=1,
+                    help="runner mode: calls per sample (the sample is their span divided by the count)")
     ap.add_argument("--profile-once", action="store_true",
                     help="runner mode: warm up, then enqueue one call without timing and print nothing")
     return ap.parse_args(argv)
@@ -278,10 +281,18 @@ def sample_stats(seconds):
             "p95_us": round(percentile(seconds, 0.95) * 1e6, 2), "cv": round(cv, 4)}
 
 
-def batch_sizes(steps, samples=20):
-    """`steps` calls split into min(samples, steps) batches whose sizes differ
-    by at most one and sum to exactly `steps`."""
-    n = max(1, min(samples, steps))
+MIN_BATCH = 10      # chains per timed sample (the reference runner's kernel_repeats role)
+SETTLE_CHAINS = 50  # untimed chains before the first sample, counting --warmup
+
+
+def batch_sizes(steps, samples=20, min_batch=MIN_BATCH):
+    """`steps` calls split into at most `samples` batches of at least
+    `min_batch` calls each (one batch when steps < min_batch), sizes differing
+    by at most one and summing to exactly `steps`. Each batch carries one
+    timing event, so its cost per call does not grow as --steps shrinks
+    (the reference runner's fixed kernel_repeats per sample,
+    benchmarks/core/runner.cpp:350-370)."""
+    n = max(1, min(samples, steps // min_batch))
     return [steps // n + (1 if i < steps % n else 0) for i in range(n)]
 
 
@@ -435,16 +446,20 @@ def launch_report(torch, device, ch, model, n=50):
 # ------------------------------------------------------------------ workloads
 
 def headline(torch, device, args):
-    """The headline chain: `--warmup` untimed chains, then exactly `--steps`
-    chains in at most 20 batches (reference runner: each sample is the event
-    span of a batch divided by its size); value = T / p50 of the batch means.
-    Then the cold chain, the graph report and the per-launch / per-stage
-    breakdown (graph_time)."""
+    """The headline chain: `--warmup` untimed chains (then more untimed chains
+    up to SETTLE_CHAINS in all: the clock needs about 50 back-to-back chains
+    to settle), then exactly `--steps` chains in batches of at least
+    MIN_BATCH (reference runner: each sample is the event span of a batch
+    divided by its size); value = T / p50 of the batch means. The outputs of
+    the last timed chain are copied to the host for validation. Then the cold
+    chain, the graph report and the per-launch / per-stage breakdown
+    (graph_time)."""
     from raggedroute_amd import workloads
     cfg = workloads.HEADLINE
     inputs = workloads.chain_inputs_device(cfg, 0, device)
     ch = Chain(cfg, inputs, device)
-    for _ in range(args.warmup):
+    settle = max(0, SETTLE_CHAINS - args.warmup)
+    for _ in range(args.warmup + settle):
         ch.chain()
     torch.cuda.synchronize()
     sizes = batch_sizes(args.steps)
@@ -452,8 +467,12 @@ def headline(torch, device, args):
     means = batch_means(torch, ch.chain, sizes=sizes)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    timed_outputs = {name: getattr(ch, attr).cpu().numpy() for name, attr in (
+        ("logits", "logits"), ("ids", "ids"), ("weights", "w"), ("counts", "counts"), ("offsets", "offsets"),
+        ("route_pos", "pos"), ("x_permuted", "xp"), ("y", "y"))}
     warm = sample_stats(means)
     warm["batch_sizes"] = sorted(set(sizes))
+    warm["clock_settle_chains"] = settle
     mean_s = sum(m * n for m, n in zip(means, sizes)) / args.steps
     cold = sample_stats(cold_spans(torch, ch, device, samples=20))
     active = int((ch.counts.cpu().numpy() > 0).sum())
@@ -464,8 +483,9 @@ def headline(torch, device, args):
     model = work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active)
     stages = stage_report(torch, device, ch, model)
     return cfg, ch, inputs, {"p50_s": percentile(means, 0.5), "mean_s": mean_s, "wall_s": wall,
-                             "warm": warm, "cold": cold, "graph": graph,
-                             "launches": launches, "stages": stages, "active_experts": active}
+                             "warm": warm, "cold": cold, "graph": graph, "samples": len(sizes),
+                             "launches": launches, "stages": stages, "active_experts": active,
+                             "timed_outputs": timed_outputs}
 
 
 def c4(torch, device, hidden=4096, output=14336, reps=5, samples=10, cpu_sample=False):
@@ -742,20 +762,87 @@ def c3(torch, device):
     return out
 
 
-def cpu_chain_seconds(inputs_host, from_tokens, runs=5):
+def cpu_chain_seconds(inputs_host, from_tokens, runs=5, keep=None):
     """Reference CPU oracle chain (oracle/, single thread, -O2
-    -ffp-contract=off), median of `runs` full runs."""
+    -ffp-contract=off), median of `runs` full runs. `keep` (a dict) receives
+    the last run's outputs."""
     import oracle
     out = []
     for _ in range(runs):
         t0 = time.perf_counter()
         if from_tokens:
-            oracle.chain(inputs_host["x"], inputs_host["expert_weights"],
-                         router_weights=inputs_host["router_weights"])
+            res = oracle.chain(inputs_host["x"], inputs_host["expert_weights"],
+                               router_weights=inputs_host["router_weights"])
         else:
-            oracle.chain(inputs_host["x"], inputs_host["expert_weights"], logits=inputs_host["logits"])
+            res = oracle.chain(inputs_host["x"], inputs_host["expert_weights"], logits=inputs_host["logits"])
         out.append(time.perf_counter() - t0)
+    if keep is not None:
+        keep.update(res)
     return statistics.median(out)
+
+
+def validate_chain(cfg, host, dev, ref):
+    """The outputs of the last timed chain_from_tokens against the oracle chain
+    run on the same inputs (the reference runner validates after measuring,
+    benchmarks/core/runner.cpp:372-381, with the chain checks of
+    benchmarks/adapters/chain_adapter.cpp:469-495). ids are exact against the
+    oracle top-2 of the device logits, the logits within the
+    accumulation-aware GEMM bound of the exact product, and ids may differ from
+    the CPU-logit oracle only on rows whose CPU rank-1/2 or rank-2/3 margin
+    lies within that bound (counted); counts, offsets, the stable route map and
+    the copied rows are exact; weights within 1e-6, y within atol 1e-4 +
+    rtol 4e-5*K."""
+    import oracle
+    t, e, k = cfg.tokens, cfg.experts, cfg.hidden
+    x, wr, we = host["x"], host["router_weights"], host["expert_weights"]
+    x64, wr64 = x.astype(np.float64), wr.astype(np.float64)
+    gamma = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+    bound = 4 * gamma * (np.abs(x64) @ np.abs(wr64)) + 1e-7
+    checks = {"logits_within_gemm_bound": bool((np.abs(dev["logits"] - x64 @ wr64) <= bound).all())}
+    ids, w = oracle.top2_f32(dev["logits"])
+    checks["ids_exact"] = bool(np.array_equal(dev["ids"], ids))
+    checks["weights_within_1e-6"] = oracle.compare_floating(dev["weights"], w, 1e-6, 1e-6)[0] == 0
+    counts = oracle.histogram(ids, e)
+    offsets = oracle.exclusive_scan(counts)
+    pos = oracle.stable_route_pos(ids, offsets)
+    checks["counts_exact"] = bool(np.array_equal(dev["counts"], counts))
+    checks["offsets_exact"] = bool(np.array_equal(dev["offsets"], offsets))
+    checks["route_pos_exact"] = bool(np.array_equal(dev["route_pos"], pos))
+    src = np.arange(2 * t) // 2
+    checks["x_permuted_exact"] = bool(np.array_equal(dev["x_permuted"][pos].view(np.uint32),
+                                                     x[src].view(np.uint32)))
+    srt = np.sort(ref["logits"].astype(np.float64), axis=1)[:, ::-1]
+    margin = np.minimum(srt[:, 0] - srt[:, 1], srt[:, 1] - srt[:, 2])
+    near = margin <= 2 * bound.max(axis=1)
+    differ = (ref["ids"] != dev["ids"]).any(axis=1)
+    checks["ids_differ_from_cpu_logits_only_on_near_ties"] = bool(near[differ].all())
+    y_fails, y_abs, y_rel = oracle.compare_floating(dev["y"], oracle.chain_output_f32(x, we, ids, w),
+                                                    1e-4, 4e-5 * k)
+    checks["y_within_chain_tolerance"] = y_fails == 0
+    return {"ok": bool(all(checks.values())), "what": "outputs of the last timed chain", "checks": checks,
+            "near_tie_rows": int(near.sum()), "id_rows_differing_from_cpu_logits": int(differ.sum()),
+            "y_failures": y_fails, "y_max_abs": y_abs, "y_max_rel": y_rel,
+            "reference": "benchmarks/core/runner.cpp:372-381; benchmarks/adapters/chain_adapter.cpp:469-495"}
+
+
+def environment(torch, device):
+    """Run environment (the reference record's environment / build fields,
+    benchmarks/core/runner.cpp:413-543): device, runtimes, and the source
+    revision the library was built from (written by the build)."""
+    props = torch.cuda.get_device_properties(device)
+    env = {"device": props.name, "arch": getattr(props, "gcnArchName", None),
+           "compute_units": props.multi_processor_count, "hbm_gib": round(props.total_memory / 2 ** 30, 1),
+           "torch": torch.__version__, "torch_hip": getattr(torch.version, "hip", None),
+           "python": sys.version.split()[0], "host_cpu": cpu_model(), "host_cpus": os.cpu_count()}
+    hip = Marks._hip
+    if hip is not None:
+        for name in ("hipRuntimeGetVersion", "hipDriverGetVersion"):
+            v = ctypes.c_int()
+            if getattr(hip, name)(ctypes.byref(v)) == 0:
+                env[name[3:].replace("GetVersion", "_version").lower()] = v.value
+    info = REPO / "raggedroute_amd" / "build_info.json"
+    env["build"] = json.loads(info.read_text()) if info.exists() else None
+    return env
 
 
 def cpu_model():
@@ -838,13 +925,21 @@ def runner_params(pairs):
 
 
 def run_runner(torch, device, args):
-    """One chain entry or operator at any shape, timed with the reference
-    runner's semantics: `--warmup` calls, then `--samples` samples, each the
-    event span of `--kernel-repeats` back-to-back calls divided by the repeat
-    count (warm), or of one call after a `--cache-scrub-bytes` scrub
-    (cold_scrub); the reported value uses the p50 sample. Prints one JSON
-    record shaped like the headline line. Outputs are not validated here: the
-    tests check every entry against the oracle."""
+    """One chain entry or operator at any shape, timed like the reference
+    runner (benchmarks/core/runner.cpp:336-370): `--warmup` iterations, then
+    `--samples` samples; each iteration and sample is `--kernel-repeats`
+    back-to-back calls, preceded in cold_scrub mode by a
+    `--cache-scrub-bytes` scrub and a synchronisation, and a sample is the
+    event span of its calls divided by the repeat count; the reported value
+    uses the p50 sample. Defaults are the reference's (types.h:71-76: warmup
+    5, samples 10, kernel_repeats 1) except the scrub size, which the
+    reference requires on the command line and which defaults to 512 MiB
+    here. Warm samples run back to back with timing-only events between them
+    (batch_means) instead of a host synchronisation per sample. Prints one
+    JSON record shaped like the headline line, with these settings under
+    "runner". Outputs are not validated in this mode (the record says so):
+    the GPU tests check every entry against the oracle, and the default
+    headline run validates its timed chain."""
     import raggedroute_amd as rr
     from raggedroute_amd import workloads
     p = runner_params(args.param)
@@ -920,26 +1015,44 @@ def run_runner(torch, device, args):
             nbytes, flops = work_model(t, e, k, n, active)[stage]
             call, unit_count, unit = (lambda: ch.stage(stage)), None, None
 
+    repeats = args.kernel_repeats
+    if repeats < 1 or args.samples < 1 or args.warmup < 0:
+        raise SystemExit("--kernel-repeats and --samples must be >= 1, --warmup >= 0")
+    scrub = None
+    if args.cache_mode == "cold_scrub":
+        if args.cache_scrub_bytes < 4:
+            raise SystemExit("cold_scrub needs --cache-scrub-bytes >= 4")
+        scrub = torch.empty(args.cache_scrub_bytes // 4, dtype=torch.int32, device=device)
+
+    def scrub_cache():
+        if scrub is not None:
+            assert rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), stream) == 0
+            torch.cuda.synchronize()
+
+    # reference benchmarks/core/runner.cpp:336-370: every warmup iteration and
+    # every sample is a scrub (cold_scrub) followed by kernel_repeats calls
     for _ in range(args.warmup):
-        call()
+        scrub_cache()
+        for _ in range(repeats):
+            call()
     torch.cuda.synchronize()
     if args.profile_once:
         call()
         torch.cuda.synchronize()
         return None
-    if args.cache_mode == "warm":
-        samples = batch_means(torch, call, samples=args.samples, repeats=args.kernel_repeats)
-        repeats = args.kernel_repeats
+    if scrub is None:
+        samples = batch_means(torch, call, samples=args.samples, repeats=repeats)
     else:
-        scrub = torch.empty(max(1, args.cache_scrub_bytes // 4), dtype=torch.int32, device=device)
         samples = []
         for _ in range(args.samples):
-            assert rr.ops.launch_cache_scrub(scrub.data_ptr(), scrub.numel(), stream) == 0
+            scrub_cache()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(); call(); b.record()
+            a.record()
+            for _ in range(repeats):
+                call()
+            b.record()
             b.synchronize()
-            samples.append(a.elapsed_time(b) / 1e3)
-        repeats = 1
+            samples.append(a.elapsed_time(b) / 1e3 / repeats)
         del scrub
     p50 = percentile(samples, 0.5)
     line = {"metric": f"{target} {'tokens/s' if unit else 'roofline rate'} @T{t}/E{e}/K{k}/N{n} FP32",
@@ -950,6 +1063,9 @@ def run_runner(torch, device, args):
                        "distribution": p["distribution"], "zipf_s": p["zipf_s"],
                        "tie_fraction": p["tie_fraction"], "variant": args.variant,
                        "cache_mode": args.cache_mode},
+            "runner": {"warmup": args.warmup, "samples": args.samples, "kernel_repeats": repeats,
+                       "cache_scrub_bytes": args.cache_scrub_bytes if args.cache_mode == "cold_scrub" else 0,
+                       "validated": False},
             "samples": sample_stats(samples)}
     if unit is not None:
         line.update(value=round(unit_count / p50, 1), unit=unit)
@@ -974,6 +1090,7 @@ def main() -> int:
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     if args.suite or args.operator:
+        args.warmup = 5 if args.warmup is None else args.warmup
         line = run_runner(torch, device, args)
         if line is not None:
             print(json.dumps(line))
@@ -981,6 +1098,7 @@ def main() -> int:
     if args.profile:
         profile(torch, device, args.profile)
         return 0
+    args.warmup = 20 if args.warmup is None else args.warmup
     cfg, ch, inputs, head = headline(torch, device, args)
     tokens_per_s = cfg.tokens / head["p50_s"]
     launches = head["launches"]
@@ -1023,11 +1141,15 @@ def main() -> int:
     elif args.route_trace:
         extras["route_trace"] = trace_replay(torch, device, args.route_trace)
 
+    # cpu_baseline leg: the oracle chain on the same headline inputs, timed
+    # (not with --quick) and used to validate the timed run (always)
     cpu = None
+    host = {k: v.cpu().numpy() for k, v in inputs.items()}
+    ref = {}
+    sec = cpu_chain_seconds(host, True, runs=1 if args.quick else 5, keep=ref)
+    validation = validate_chain(cfg, host, head["timed_outputs"], ref)
     if not args.quick:
         from raggedroute_amd import workloads
-        host = {k: v.cpu().numpy() for k, v in inputs.items()}
-        sec = cpu_chain_seconds(host, True)
         others = {}
         for c in (workloads.C1, workloads.C2):
             sec_c = cpu_chain_seconds(workloads.chain_inputs(c, 0), c.from_tokens)
@@ -1053,6 +1175,12 @@ def main() -> int:
         "ms_per_step": round(head["p50_s"] * 1e3, 5),
         "mean_chain_us": round(head["mean_s"] * 1e6, 2),
         "chain_warm": head["warm"],
+        "validation": validation,
+        "release_gate": {"ok": args.warmup >= 10 and head["samples"] >= 20 and validation["ok"],
+                         "warmup": args.warmup, "samples": head["samples"], "validated": validation["ok"],
+                         "requires": "warmup >= 10, samples >= 20, validation after measurement "
+                                     "(reference benchmarks/core/runner.cpp:293-312)"},
+        "environment": environment(torch, device),
         "chain_cold": head["cold"],
         "chain_graph": head["graph"],
         "higher_is_better": True,
@@ -1069,6 +1197,9 @@ def main() -> int:
         "extras": extras,
     }
     print(json.dumps(line))
+    if not validation["ok"]:
+        print("post-benchmark validation failed: " + json.dumps(validation["checks"]), file=sys.stderr)
+        return 3
     return 0
 
 

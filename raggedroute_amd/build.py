@@ -13,6 +13,8 @@ library, which does not exist yet on a fresh checkout.
 from __future__ import annotations
 
 import concurrent.futures
+import datetime
+import json
 import os
 import shutil
 import subprocess
@@ -26,6 +28,9 @@ INCLUDE = REPO / "include"
 BUILD = REPO / "_build"
 LIB_NAME = "libraggedroute_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# Source revision and toolchain of the last build (git-ignored like the
+# library, and shipped beside it): benchmark records name what they ran.
+BUILD_INFO = PKG_DIR / "build_info.json"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
@@ -72,6 +77,23 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _git(*args: str) -> str | None:
+    try:
+        proc = subprocess.run(["git", "-C", str(REPO), *args], capture_output=True, text=True, timeout=30)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return proc.stdout.strip() if proc.returncode == 0 else None
+
+
+def _build_info() -> dict:
+    hipcc = subprocess.run([_hipcc(), "--version"], capture_output=True, text=True)
+    version = next((line.strip() for line in hipcc.stdout.splitlines() if line.startswith("HIP version")), None)
+    status = _git("status", "--porcelain", "--untracked-files=no")
+    return {"git_sha": _git("rev-parse", "HEAD"), "git_dirty": None if status is None else bool(status),
+            "built_utc": datetime.datetime.now(datetime.timezone.utc).strftime("%Y-%m-%dT%H:%M:%SZ"),
+            "hip": version, "arch": ARCH, "hip_flags": " ".join(HIP_FLAGS)}
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     """Compile every source and link the shared library; returns its path."""
     BUILD.mkdir(exist_ok=True)
@@ -86,6 +108,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
           *map(str, objects), f"-L{ROCM / 'lib'}", "-lamdhip64",
           f"-Wl,-rpath,{ROCM / 'lib'}"])
     shutil.move(str(tmp), str(LIB_PATH))
+    BUILD_INFO.write_text(json.dumps(_build_info(), indent=1) + "\n")
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH

@@ -33,7 +33,7 @@ rr_mutable_tensor_view mview(void* data) noexcept { return {data, default_spec()
 rr_status validate_chain(const rr_chain_args* a, const rr_runtime_context* context,
                          bool from_tokens) noexcept {
   if (a == nullptr) return invalid_argument("chain args must not be null");
-  if (context == nullptr) return invalid_argument("runtime context must not be null");
+  if (context == nullptr) return invalid_argument("no runtime context was given");
   if (a->tokens < 0 || a->experts < 2 || a->experts > RR_MAX_EXPERTS || a->top_k != 2 ||
       a->hidden < 0 || a->output < 0) {
     return invalid_argument("chain requires T>=0, 2<=E<=1024, top_k=2, K>=0 and N>=0");
@@ -250,7 +250,7 @@ rr_status run_chain(const rr_chain_args* a, const rr_runtime_context* context,
 rr_status validate_route_chain(const rr_route_chain_args* a,
                                const rr_runtime_context* context) noexcept {
   if (a == nullptr) return invalid_argument("route chain args must not be null");
-  if (context == nullptr) return invalid_argument("runtime context must not be null");
+  if (context == nullptr) return invalid_argument("no runtime context was given");
   if (a->tokens < 0 || a->experts < 1 || a->experts > RR_MAX_EXPERTS || a->top_k < 1 ||
       a->top_k > a->experts || a->top_k > 64 || a->hidden < 0 || a->output < 0) {
     return invalid_argument(

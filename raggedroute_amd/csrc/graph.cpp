@@ -42,7 +42,7 @@ bool optimized_family(const rr_kernel_selection& k) noexcept {
 
 rr_status check_call(int32_t entry, const void* args, const rr_runtime_context* context) noexcept {
   if (args == nullptr) return invalid_argument("chain graph args must not be null");
-  if (context == nullptr) return invalid_argument("runtime context must not be null");
+  if (context == nullptr) return invalid_argument("no runtime context was given");
   if (context->stream == nullptr) {
     return invalid_argument("chain graph capture needs a non-default stream");
   }

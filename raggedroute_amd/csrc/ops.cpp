@@ -34,7 +34,7 @@ rr_status unknown_family(const char* message) noexcept {
   return make_status(RR_STATUS_UNSUPPORTED_KERNEL_VARIANT, message);
 }
 
-rr_status null_context() noexcept { return invalid_argument("runtime context must not be null"); }
+rr_status null_context() noexcept { return invalid_argument("no runtime context was given"); }
 
 }  // namespace
 }  // namespace rr
@@ -73,13 +73,13 @@ size_t rr_route_chain_workspace_size(const rr_route_chain_args* args) {
 
 // reference src/dense_gemm/operator.cpp:18-58
 rr_status rr_dense_gemm(const rr_dense_gemm_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("dense_gemm args must not be null");
+  if (args == nullptr) return rr::invalid_argument("dense_gemm: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->m < 0 || args->n < 0 || args->k < 0) {
-    return rr::invalid_argument("dense_gemm dimensions must be non-negative");
+    return rr::invalid_argument("dense_gemm: m, n and k must be >= 0");
   }
   if (args->alpha != 1.0F || args->beta != 0.0F) {
-    return rr::invalid_argument("dense_gemm supports alpha=1 and beta=0 only");
+    return rr::invalid_argument("dense_gemm: only alpha = 1 with beta = 0 is implemented");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(
@@ -89,12 +89,12 @@ rr_status rr_dense_gemm(const rr_dense_gemm_args* args, const rr_runtime_context
   if (args->m == 0 || args->n == 0) return rr::ok_status();
   if (args->c.data == nullptr ||
       (args->k != 0 && (args->a.data == nullptr || args->b.data == nullptr))) {
-    return rr::invalid_argument("dense_gemm received a null device pointer");
+    return rr::invalid_argument("dense_gemm: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->a.data, alignof(float)) ||
       !rr::is_aligned(args->b.data, alignof(float)) ||
       !rr::is_aligned(args->c.data, alignof(float))) {
-    return rr::invalid_argument("dense_gemm FP32 buffers must be 4-byte aligned");
+    return rr::invalid_argument("dense_gemm: every buffer must start on a 4-byte boundary");
   }
   const auto* a = static_cast<const float*>(args->a.data);
   const auto* b = static_cast<const float*>(args->b.data);
@@ -102,28 +102,28 @@ rr_status rr_dense_gemm(const rr_dense_gemm_args* args, const rr_runtime_context
   if (decision.kernel.family == RR_FAMILY_NAIVE) {
     return rr::device_status(rr::kern::dense_gemm_naive(a, b, c, args->m, args->n, args->k,
                                                         context->stream),
-                             "dense_gemm naive kernel launch failed");
+                             "dense_gemm: the naive kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(
         rr::kern::dense_gemm_mfma(a, b, c, args->m, args->n, args->k, context->stream),
-        "dense_gemm gfx950 kernel launch failed");
+        "dense_gemm: the gfx950 kernel did not launch");
   }
-  return rr::unknown_family("dense_gemm dispatch selected an unknown kernel family");
+  return rr::unknown_family("dense_gemm: no kernel exists for the selected family");
 }
 
 // reference src/topk_gate/operator.cpp:18-60
 rr_status rr_topk_gate(const rr_topk_gate_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("topk_gate args must not be null");
+  if (args == nullptr) return rr::invalid_argument("topk_gate: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->tokens < 0 || args->experts < 2 || args->experts > RR_MAX_EXPERTS ||
       args->top_k != 2) {
-    return rr::invalid_argument("topk_gate requires tokens>=0, 2<=E<=1024, and top_k=2");
+    return rr::invalid_argument("topk_gate: needs tokens >= 0, 2 <= experts <= 1024 and top_k == 2");
   }
   if (args->normalization != RR_TOPK_SELECTED_SOFTMAX ||
       args->tie_break != RR_TOPK_TIE_LOWER_EXPERT_ID ||
       args->nan_policy != RR_TOPK_NAN_NEG_INF_ALL_NAN_01) {
-    return rr::invalid_argument("topk_gate received unsupported semantic policy");
+    return rr::invalid_argument("topk_gate: only the reference tie, NaN and normalisation policies are implemented");
   }
   rr_operator_signature signature{};
   signature.has_input = 1;
@@ -139,11 +139,11 @@ rr_status rr_topk_gate(const rr_topk_gate_args* args, const rr_runtime_context* 
   if (args->tokens == 0) return rr::ok_status();
   if (args->logits.data == nullptr || args->expert_ids == nullptr ||
       args->weights.data == nullptr) {
-    return rr::invalid_argument("topk_gate received a null device pointer");
+    return rr::invalid_argument("topk_gate: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->logits.data, alignof(float)) ||
       !rr::is_aligned(args->weights.data, alignof(float))) {
-    return rr::invalid_argument("topk_gate FP32 buffers must be 4-byte aligned");
+    return rr::invalid_argument("topk_gate: every buffer must start on a 4-byte boundary");
   }
   const auto* logits = static_cast<const float*>(args->logits.data);
   auto* weights = static_cast<float*>(args->weights.data);
@@ -155,98 +155,98 @@ rr_status rr_topk_gate(const rr_topk_gate_args* args, const rr_runtime_context* 
     error = rr::kern::topk_gate_wave(logits, args->expert_ids, weights, args->tokens,
                                      args->experts, context->stream);
   } else {
-    return rr::unknown_family("topk_gate dispatch selected an unsupported kernel");
+    return rr::unknown_family("topk_gate: no kernel exists for the selected family");
   }
-  return rr::device_status(error, "topk_gate kernel launch failed");
+  return rr::device_status(error, "topk_gate: a kernel did not launch");
 }
 
 // reference src/histogram/operator.cpp:20-57
 rr_status rr_histogram(const rr_histogram_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("histogram args must not be null");
+  if (args == nullptr) return rr::invalid_argument("histogram: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->route_pairs < 0 || args->experts <= 0 || args->experts > RR_MAX_EXPERTS) {
-    return rr::invalid_argument("histogram requires route_pairs>=0 and 1<=E<=1024");
+    return rr::invalid_argument("histogram: needs route_pairs >= 0 and 1 <= experts <= 1024");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(RR_OP_HISTOGRAM, {}, args->kernel,
                                            context->architecture, &decision);
   if (status.code != RR_STATUS_SUCCESS) return status;
   if (args->counts == nullptr || (args->route_pairs != 0 && args->expert_ids == nullptr)) {
-    return rr::invalid_argument("histogram received a null device pointer");
+    return rr::invalid_argument("histogram: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->counts, alignof(int32_t)) ||
       !rr::is_aligned(args->expert_ids, alignof(int32_t))) {
-    return rr::invalid_argument("histogram buffers must be 4-byte aligned");
+    return rr::invalid_argument("histogram: every buffer must start on a 4-byte boundary");
   }
   if (decision.kernel.family == RR_FAMILY_NAIVE) {
     // The naive launcher accumulates, so the wrapper owns the reset.
     status = rr::device_status(
         hipMemsetAsync(args->counts, 0, static_cast<size_t>(args->experts) * sizeof(int32_t),
                        context->stream),
-        "histogram counts reset failed");
+        "histogram: clearing the counts failed");
     if (status.code != RR_STATUS_SUCCESS) return status;
     return rr::device_status(rr::kern::histogram_naive(args->expert_ids, args->counts,
                                                        args->route_pairs, args->experts,
                                                        context->stream),
-                             "histogram kernel launch failed");
+                             "histogram: a kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(rr::kern::histogram_native(args->expert_ids, args->counts,
                                                         args->route_pairs, args->experts,
                                                         context->stream),
-                             "histogram kernel launch failed");
+                             "histogram: a kernel did not launch");
   }
-  return rr::unknown_family("histogram dispatch selected an unknown kernel");
+  return rr::unknown_family("histogram: no kernel exists for the selected family");
 }
 
 // reference src/scan/operator.cpp:51-74
 rr_status rr_exclusive_scan(const rr_exclusive_scan_args* args,
                             const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("exclusive_scan args must not be null");
+  if (args == nullptr) return rr::invalid_argument("exclusive_scan: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->experts <= 0 || args->experts > RR_MAX_EXPERTS) {
-    return rr::invalid_argument("exclusive_scan requires 1<=E<=1024");
+    return rr::invalid_argument("exclusive_scan: needs 1 <= experts <= 1024");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(RR_OP_EXCLUSIVE_SCAN, {}, args->kernel,
                                            context->architecture, &decision);
   if (status.code != RR_STATUS_SUCCESS) return status;
   if (args->counts == nullptr || args->offsets == nullptr) {
-    return rr::invalid_argument("exclusive_scan received a null device pointer");
+    return rr::invalid_argument("exclusive_scan: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->counts, alignof(int32_t)) ||
       !rr::is_aligned(args->offsets, alignof(int32_t))) {
-    return rr::invalid_argument("exclusive_scan buffers must be 4-byte aligned");
+    return rr::invalid_argument("exclusive_scan: every buffer must start on a 4-byte boundary");
   }
   if (decision.kernel.family == RR_FAMILY_NAIVE) {
     return rr::device_status(rr::kern::exclusive_scan_naive(args->counts, args->offsets,
                                                             args->experts, context->stream),
-                             "exclusive_scan naive kernel launch failed");
+                             "exclusive_scan: the naive kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(rr::kern::exclusive_scan_native(args->counts, args->offsets,
                                                              args->experts, context->stream),
-                             "exclusive_scan kernel launch failed");
+                             "exclusive_scan: a kernel did not launch");
   }
-  return rr::unknown_family("exclusive_scan dispatch selected an unknown kernel");
+  return rr::unknown_family("exclusive_scan: no kernel exists for the selected family");
 }
 
 // reference src/scan/operator.cpp:84-134
 rr_status rr_histogram_exclusive_scan(const rr_histogram_exclusive_scan_args* args,
                                       const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("histogram_exclusive_scan args must not be null");
+  if (args == nullptr) return rr::invalid_argument("histogram_exclusive_scan: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->route_pairs < 0 || args->experts <= 0 || args->experts > RR_MAX_EXPERTS) {
-    return rr::invalid_argument("histogram_exclusive_scan requires route_pairs>=0 and 1<=E<=1024");
+    return rr::invalid_argument("histogram_exclusive_scan: needs route_pairs >= 0 and 1 <= experts <= 1024");
   }
   if (args->counts == nullptr || args->offsets == nullptr ||
       (args->route_pairs != 0 && args->expert_ids == nullptr)) {
-    return rr::invalid_argument("histogram_exclusive_scan received a null device pointer");
+    return rr::invalid_argument("histogram_exclusive_scan: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->expert_ids, alignof(int32_t)) ||
       !rr::is_aligned(args->counts, alignof(int32_t)) ||
       !rr::is_aligned(args->offsets, alignof(int32_t))) {
-    return rr::invalid_argument("histogram_exclusive_scan buffers must be 4-byte aligned");
+    return rr::invalid_argument("histogram_exclusive_scan: every buffer must start on a 4-byte boundary");
   }
   const size_t ids_bytes = static_cast<size_t>(args->route_pairs) * sizeof(int32_t);
   const size_t counts_bytes = static_cast<size_t>(args->experts) * sizeof(int32_t);
@@ -255,7 +255,7 @@ rr_status rr_histogram_exclusive_scan(const rr_histogram_exclusive_scan_args* ar
       rr::ranges_overlap(args->expert_ids, ids_bytes, args->offsets, offsets_bytes) ||
       rr::ranges_overlap(args->counts, counts_bytes, args->offsets, offsets_bytes)) {
     return rr::invalid_argument(
-        "histogram_exclusive_scan input and outputs must be pairwise non-overlapping");
+        "histogram_exclusive_scan: ids, counts and offsets must not overlap");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(RR_OP_HISTOGRAM_EXCLUSIVE_SCAN, {}, args->kernel,
@@ -264,38 +264,38 @@ rr_status rr_histogram_exclusive_scan(const rr_histogram_exclusive_scan_args* ar
   if (decision.kernel.family == RR_FAMILY_NAIVE) {
     // Separate path: reset + naive histogram, then naive scan.
     status = rr::device_status(hipMemsetAsync(args->counts, 0, counts_bytes, context->stream),
-                               "histogram counts reset failed");
+                               "histogram: clearing the counts failed");
     if (status.code != RR_STATUS_SUCCESS) return status;
     status = rr::device_status(rr::kern::histogram_naive(args->expert_ids, args->counts,
                                                          args->route_pairs, args->experts,
                                                          context->stream),
-                               "histogram kernel launch failed");
+                               "histogram: a kernel did not launch");
     if (status.code != RR_STATUS_SUCCESS) return status;
     return rr::device_status(rr::kern::exclusive_scan_naive(args->counts, args->offsets,
                                                             args->experts, context->stream),
-                             "exclusive_scan naive kernel launch failed");
+                             "exclusive_scan: the naive kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(
         rr::kern::histogram_exclusive_scan_native(args->expert_ids, args->counts, args->offsets,
                                                   args->route_pairs, args->experts,
                                                   context->stream),
-        "histogram_exclusive_scan kernel launch failed");
+        "histogram_exclusive_scan: a kernel did not launch");
   }
-  return rr::unknown_family("histogram_exclusive_scan selected an unknown kernel");
+  return rr::unknown_family("histogram_exclusive_scan: no kernel exists for the selected family");
 }
 
 // reference src/permute/operator.cpp:22-83
 rr_status rr_token_permute(const rr_token_permute_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("token_permute args must not be null");
+  if (args == nullptr) return rr::invalid_argument("token_permute: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->tokens < 0 || args->experts <= 0 || args->experts > RR_MAX_EXPERTS ||
       args->top_k <= 0 || args->top_k > args->experts || args->hidden < 0) {
     return rr::invalid_argument(
-        "token_permute requires T>=0, 1<=top_k<=E<=1024, and hidden>=0");
+        "token_permute: needs tokens >= 0, 1 <= top_k <= experts <= 1024 and hidden >= 0");
   }
   if (args->tokens > 0 && args->tokens > INT_MAX / args->top_k) {
-    return rr::invalid_argument("token_permute route count exceeds int32 indexing");
+    return rr::invalid_argument("token_permute: tokens * top_k does not fit in int32");
   }
   rr_operator_signature signature{};
   signature.has_input = 1;
@@ -309,19 +309,19 @@ rr_status rr_token_permute(const rr_token_permute_args* args, const rr_runtime_c
   if (args->tokens == 0) return rr::ok_status();
   if (args->expert_ids == nullptr || args->offsets == nullptr || args->route_pos == nullptr ||
       (args->hidden != 0 && (args->x.data == nullptr || args->x_permuted.data == nullptr))) {
-    return rr::invalid_argument("token_permute received a null device pointer");
+    return rr::invalid_argument("token_permute: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->x.data, alignof(float)) ||
       !rr::is_aligned(args->x_permuted.data, alignof(float))) {
-    return rr::invalid_argument("token_permute FP32 buffers must be 4-byte aligned");
+    return rr::invalid_argument("token_permute: every buffer must start on a 4-byte boundary");
   }
   const size_t workspace_bytes = static_cast<size_t>(args->experts) * sizeof(int32_t);
   if (context->workspace == nullptr || context->workspace_bytes < workspace_bytes) {
     return rr::make_status(RR_STATUS_INSUFFICIENT_WORKSPACE,
-                           "token_permute requires int32 cursor workspace for every expert");
+                           "token_permute: the workspace must hold one int32 cursor per expert");
   }
   if (!rr::is_aligned(context->workspace, alignof(int32_t))) {
-    return rr::invalid_argument("token_permute workspace is not int32 aligned");
+    return rr::invalid_argument("token_permute: the workspace must start on a 4-byte boundary");
   }
   const auto* x = static_cast<const float*>(args->x.data);
   auto* x_permuted = static_cast<float*>(args->x_permuted.data);
@@ -329,13 +329,13 @@ rr_status rr_token_permute(const rr_token_permute_args* args, const rr_runtime_c
   if (decision.kernel.family == RR_FAMILY_NAIVE) {
     // The naive launcher increments cursors atomically; the wrapper resets them.
     status = rr::device_status(hipMemsetAsync(cursors, 0, workspace_bytes, context->stream),
-                               "token_permute cursor reset failed");
+                               "token_permute: clearing the cursors failed");
     if (status.code != RR_STATUS_SUCCESS) return status;
     return rr::device_status(
         rr::kern::token_permute_naive(x, args->expert_ids, args->offsets, cursors, x_permuted,
                                       args->route_pos, args->sorted_route, args->tokens,
                                       args->top_k, args->hidden, args->experts, context->stream),
-        "token_permute naive kernel launch failed");
+        "token_permute: the naive kernel did not launch");
   }
   if (rr::is_native(decision)) {
     // The stable kernel writes the final cursor values itself (no reset pass).
@@ -344,18 +344,18 @@ rr_status rr_token_permute(const rr_token_permute_args* args, const rr_runtime_c
                                        args->route_pos, args->sorted_route, args->tokens,
                                        args->experts, args->top_k, args->hidden,
                                        context->stream),
-        "token_permute kernel launch failed");
+        "token_permute: a kernel did not launch");
   }
-  return rr::unknown_family("token_permute dispatch selected an unknown kernel family");
+  return rr::unknown_family("token_permute: no kernel exists for the selected family");
 }
 
 // reference src/grouped_gemm/operator.cpp:17-49
 rr_status rr_grouped_gemm(const rr_grouped_gemm_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("grouped_gemm args must not be null");
+  if (args == nullptr) return rr::invalid_argument("grouped_gemm: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->experts <= 0 || args->experts > RR_MAX_EXPERTS || args->hidden < 0 ||
       args->output < 0 || args->max_expert_tokens < 0) {
-    return rr::invalid_argument("grouped_gemm requires 1<=E<=1024 and non-negative dimensions");
+    return rr::invalid_argument("grouped_gemm: needs 1 <= experts <= 1024 and hidden, output, max_expert_tokens >= 0");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(
@@ -368,12 +368,12 @@ rr_status rr_grouped_gemm(const rr_grouped_gemm_args* args, const rr_runtime_con
   if (args->offsets == nullptr || args->y_permuted.data == nullptr ||
       (args->hidden != 0 &&
        (args->x_permuted.data == nullptr || args->expert_weights.data == nullptr))) {
-    return rr::invalid_argument("grouped_gemm received a null device pointer");
+    return rr::invalid_argument("grouped_gemm: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->x_permuted.data, alignof(float)) ||
       !rr::is_aligned(args->expert_weights.data, alignof(float)) ||
       !rr::is_aligned(args->y_permuted.data, alignof(float))) {
-    return rr::invalid_argument("grouped_gemm FP32 buffers must be 4-byte aligned");
+    return rr::invalid_argument("grouped_gemm: every buffer must start on a 4-byte boundary");
   }
   const auto* x = static_cast<const float*>(args->x_permuted.data);
   const auto* w = static_cast<const float*>(args->expert_weights.data);
@@ -382,29 +382,29 @@ rr_status rr_grouped_gemm(const rr_grouped_gemm_args* args, const rr_runtime_con
     return rr::device_status(
         rr::kern::grouped_gemm_naive(x, w, args->offsets, y, args->experts, args->hidden,
                                      args->output, args->max_expert_tokens, context->stream),
-        "grouped_gemm kernel launch failed");
+        "grouped_gemm: a kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(
         rr::kern::grouped_gemm_mfma(x, w, args->offsets, y, args->experts, args->hidden,
                                     args->output, args->max_expert_tokens, context->stream),
-        "grouped_gemm kernel launch failed");
+        "grouped_gemm: a kernel did not launch");
   }
-  return rr::unknown_family("grouped_gemm dispatch selected an unknown kernel family");
+  return rr::unknown_family("grouped_gemm: no kernel exists for the selected family");
 }
 
 // reference src/unpermute/operator.cpp:19-57
 rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("unpermute args must not be null");
+  if (args == nullptr) return rr::invalid_argument("unpermute: no argument struct was given");
   if (context == nullptr) return rr::null_context();
   if (args->tokens < 0 || args->top_k <= 0 || args->top_k > 64 || args->output < 0) {
-    return rr::invalid_argument("unpermute requires tokens>=0, 1<=top_k<=64, and output>=0");
+    return rr::invalid_argument("unpermute: needs tokens >= 0, 1 <= top_k <= 64 and output >= 0");
   }
   if (args->tokens > 0 && args->tokens > INT_MAX / args->top_k) {
-    return rr::invalid_argument("unpermute route count exceeds int32 indexing");
+    return rr::invalid_argument("unpermute: tokens * top_k does not fit in int32");
   }
   if (args->tokens > 0 && args->output > 0 && args->tokens > INT_MAX / args->output) {
-    return rr::invalid_argument("unpermute output count exceeds int32 indexing");
+    return rr::invalid_argument("unpermute: tokens * output does not fit in int32");
   }
   rr_dispatch_decision decision{};
   rr_status status = rr::dispatch_operator(
@@ -416,12 +416,12 @@ rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* 
   if (args->tokens == 0 || args->output == 0) return rr::ok_status();
   if (args->y_permuted.data == nullptr || args->route_pos == nullptr ||
       args->route_weights.data == nullptr || args->y.data == nullptr) {
-    return rr::invalid_argument("unpermute received a null device pointer");
+    return rr::invalid_argument("unpermute: a buffer the call reads or writes is a null pointer");
   }
   if (!rr::is_aligned(args->y_permuted.data, alignof(float)) ||
       !rr::is_aligned(args->route_weights.data, alignof(float)) ||
       !rr::is_aligned(args->y.data, alignof(float))) {
-    return rr::invalid_argument("unpermute FP32 buffers must be 4-byte aligned");
+    return rr::invalid_argument("unpermute: every buffer must start on a 4-byte boundary");
   }
   const auto* yp = static_cast<const float*>(args->y_permuted.data);
   const auto* w = static_cast<const float*>(args->route_weights.data);
@@ -430,15 +430,15 @@ rr_status rr_unpermute(const rr_unpermute_args* args, const rr_runtime_context* 
     return rr::device_status(rr::kern::unpermute_naive(yp, args->route_pos, w, y, args->tokens,
                                                        args->top_k, args->output,
                                                        context->stream),
-                             "unpermute kernel launch failed");
+                             "unpermute: a kernel did not launch");
   }
   if (rr::is_native(decision)) {
     return rr::device_status(rr::kern::unpermute_gather(yp, args->route_pos, w, y, args->tokens,
                                                         args->top_k, args->output,
                                                         context->stream),
-                             "unpermute kernel launch failed");
+                             "unpermute: a kernel did not launch");
   }
-  return rr::unknown_family("unpermute dispatch selected an unknown kernel family");
+  return rr::unknown_family("unpermute: no kernel exists for the selected family");
 }
 
 }  // extern "C"

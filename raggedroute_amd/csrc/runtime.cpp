@@ -157,12 +157,12 @@ int32_t rr_classify_gcn_arch_name(const char* name) {
 
 rr_status rr_query_current_device_architecture(int32_t* architecture) {
   if (architecture == nullptr) {
-    return rr::invalid_argument("architecture output must not be null");
+    return rr::invalid_argument("no architecture output pointer was given");
   }
   int device = 0;
   hipError_t error = hipGetDevice(&device);
   if (error != hipSuccess) {
-    return rr::device_status(error, "hipGetDevice failed while resolving architecture");
+    return rr::device_status(error, "resolving the architecture: hipGetDevice failed");
   }
   if (device >= 0 && device < rr::kMaxCachedDevices) {
     const int32_t cached = rr::g_arch_cache[device].load(std::memory_order_acquire);
@@ -174,7 +174,7 @@ rr_status rr_query_current_device_architecture(int32_t* architecture) {
   hipDeviceProp_t properties{};
   error = hipGetDeviceProperties(&properties, device);
   if (error != hipSuccess) {
-    return rr::device_status(error, "hipGetDeviceProperties failed while resolving architecture");
+    return rr::device_status(error, "resolving the architecture: hipGetDeviceProperties failed");
   }
   const int32_t arch = rr_classify_gcn_arch_name(properties.gcnArchName);
   if (device >= 0 && device < rr::kMaxCachedDevices) {
@@ -186,7 +186,7 @@ rr_status rr_query_current_device_architecture(int32_t* architecture) {
 
 rr_status rr_resolve_device_architecture(int32_t requested, int32_t* resolved) {
   if (resolved == nullptr) {
-    return rr::invalid_argument("resolved architecture output must not be null");
+    return rr::invalid_argument("no resolved-architecture output pointer was given");
   }
   if (requested == RR_ARCH_AUTO) return rr_query_current_device_architecture(resolved);
   *resolved = requested;
@@ -194,47 +194,47 @@ rr_status rr_resolve_device_architecture(int32_t requested, int32_t* resolved) {
 }
 
 rr_status rr_select_kernel(const rr_dispatch_request* request, rr_dispatch_decision* decision) {
-  if (decision == nullptr) return rr::invalid_argument("dispatch decision output must not be null");
-  if (request == nullptr) return rr::invalid_argument("dispatch request must not be null");
+  if (decision == nullptr) return rr::invalid_argument("select_kernel: no decision output pointer was given");
+  if (request == nullptr) return rr::invalid_argument("select_kernel: no request was given");
   const int32_t kind = request->operator_kind;
   if (kind < RR_OP_DENSE_GEMM || kind > RR_OP_HISTOGRAM_EXCLUSIVE_SCAN) {
-    return rr::invalid_argument("unknown operator kind");
+    return rr::invalid_argument("select_kernel: the operator kind is not one of the eight operators");
   }
   const rr_operator_signature& s = request->signature;
   if (!rr::roles_valid(kind, s)) {
-    return rr::invalid_argument("dispatch signature roles do not match the operator");
+    return rr::invalid_argument("select_kernel: the signature's input / weight / accumulator / output roles do not fit the operator");
   }
   if (!rr::has_v02_layout(s.has_input, s.input) || !rr::has_v02_layout(s.has_weight, s.weight) ||
       !rr::has_v02_layout(s.has_output, s.output)) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_LAYOUT,
-                           "v0.2 dispatch requires zero-stride contiguous row-major tensors");
+                           "select_kernel: tensors must be contiguous row-major with zero strides");
   }
   if (!rr::dtype_signature_valid(kind, s) || !rr::all_fp32(s)) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_DATA_TYPE,
-                           "the requested dtype signature has no v0.2 kernel");
+                           "select_kernel: only all-FP32 signatures have kernels");
   }
   if (request->architecture == RR_ARCH_AUTO) {
-    return rr::invalid_argument("select_kernel requires a resolved architecture");
+    return rr::invalid_argument("select_kernel: resolve the architecture (kAuto) before selecting");
   }
   if (request->architecture != RR_ARCH_GFX950) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_ARCHITECTURE,
-                           "this build executes on gfx950 (MI355X) only");
+                           "select_kernel: kernels exist for gfx950 (MI355X) only");
   }
   const rr_kernel_selection requested = request->requested_kernel;
   if (requested.family == RR_FAMILY_AUTO && requested.implementation_id != 0) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_KERNEL_VARIANT,
-                           "automatic kernel selection requires implementation_id=0");
+                           "select_kernel: the auto family takes implementation id 0 only");
   }
   if (requested.family == RR_FAMILY_NAIVE && requested.implementation_id != 0) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_KERNEL_VARIANT,
-                           "the naive family has no non-default implementation");
+                           "select_kernel: the naive family takes implementation id 0 only");
   }
   decision->operator_kind = kind;
   decision->architecture = RR_ARCH_GFX950;
   if (requested.family == RR_FAMILY_OPTIMIZED) {
     if (!rr::optimized_id_accepted(kind, requested.implementation_id)) {
       return rr::make_status(RR_STATUS_UNSUPPORTED_KERNEL_VARIANT,
-                             "requested optimized kernel is not implemented");
+                             "select_kernel: no optimized kernel has that implementation id");
     }
     decision->kernel = requested;
     return rr::ok_status();
@@ -245,7 +245,7 @@ rr_status rr_select_kernel(const rr_dispatch_request* request, rr_dispatch_decis
   }
   if (requested.family != RR_FAMILY_AUTO) {
     return rr::make_status(RR_STATUS_UNSUPPORTED_KERNEL_VARIANT,
-                           "requested kernel family is not implemented");
+                           "select_kernel: the kernel family is not one of auto / naive / optimized");
   }
   decision->kernel = {RR_FAMILY_OPTIMIZED, RR_IMPL_GFX950_NATIVE};
   return rr::ok_status();
