@@ -230,35 +230,37 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
                                                     int total, int grid, int worker, int cap) {
   static_assert(U == 1 || U == 2, "whole or half strips");
   const int lane = lane_id();
-  const int m0 = total > 0 ? (U * total + grid - 1) / grid : U;
-  const int m1 = m0 + 1;
-  auto need = [&](int m) {
-    int32_t n = 0;
+  const int m0 = total > 0 ? ceil_div32(U * total, grid) : U;
+  // units (strips or half strips) of each lane's segments, computed once
+  int32_t units[kMaxBlocks];
 #pragma unroll
-    for (int j = 0; j < kMaxBlocks; ++j) {
-      if (j < nblk) n += wave_sum(ceil_div32(U * strips_of(t.cnt[j]), m));
-    }
-    return n;
-  };
+  for (int j = 0; j < kMaxBlocks; ++j) units[j] = j < nblk ? U * strips_of(t.cnt[j]) : 0;
   // m halves touch at most m / 2 + 1 strips (+1 when the range starts with a right half)
   auto fits_cap = [&](int m) { return (U == 2 ? m / 2 + 1 : m) <= cap; };
-  const bool fit0 = fits_cap(m0) && need(m0) <= grid;
-  const bool fit1 = !fit0 && fits_cap(m1) && need(m1) <= grid;  // (only asked when m0 fails)
-  if (!fit0 && !fit1) return even_range(total, grid, worker);
-  const int m = fit0 ? m0 : m1;
-  // workers of segment e: [wpre_e, wpre_e + ceil(2 strips_e / m))
+  // workers of segment e: [wpre_e, wpre_e + ceil(units_e / m)); the scans'
+  // totals say whether m fits the grid (m0 first, m0 + 1 only when m0 fails)
   int32_t wpre[kMaxBlocks];
-  int32_t carry = 0;
+  auto workers_for = [&](int m) {
+    int32_t carry = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxBlocks; ++j) {
-    if (j < nblk) {
-      const int32_t wk = ceil_div32(U * strips_of(t.cnt[j]), m);
-      const int32_t incl = rr::dev::wave_inclusive_scan(wk);
-      wpre[j] = carry + incl - wk;
-      carry += __builtin_amdgcn_readlane(incl, 63);
-    } else {
-      wpre[j] = INT_MAX;
+    for (int j = 0; j < kMaxBlocks; ++j) {
+      if (j < nblk) {
+        const int32_t wk = ceil_div32(units[j], m);
+        const int32_t incl = rr::dev::wave_inclusive_scan(wk);
+        wpre[j] = carry + incl - wk;
+        carry += __builtin_amdgcn_readlane(incl, 63);
+      } else {
+        wpre[j] = INT_MAX;
+      }
     }
+    return carry;
+  };
+  int m = m0;
+  int carry = fits_cap(m0) ? workers_for(m0) : INT_MAX;
+  if (carry > grid) {
+    m = m0 + 1;
+    carry = fits_cap(m) ? workers_for(m) : INT_MAX;
+    if (carry > grid) return even_range(total, grid, worker);
   }
   StripRange r;
   r.s0 = r.s1 = r.h0 = r.h1 = 0;
@@ -277,12 +279,23 @@ __device__ __forceinline__ StripRange assign_strips(const SegTable& t, int nblk,
     const int first = seg_field(wpre, nblk, e);
     const int pre_e = seg_field(t.pre, nblk, e);
     const int cnt_e = seg_field(t.cnt, nblk, e);
-    const int units = U * strips_of(cnt_e);
-    const int workers = ceil_div32(units, m);  // >= 1: worker lies in this segment
+    const int units_e = U * strips_of(cnt_e);
+    const int workers = ceil_div32(units_e, m);  // >= 1: worker lies in this segment
     const int j = worker - first;
-    // even share: units [j H / w, (j + 1) H / w)
-    const int lo = static_cast<int>(static_cast<long long>(j) * units / workers) * (2 / U);
-    const int hi = static_cast<int>(static_cast<long long>(j + 1) * units / workers) * (2 / U);
+    // even share: units [j H / w, (j + 1) H / w); j < w <= grid, so for
+    // grid <= 2^8 the products fit 32 bits below H = 2^24 (every chain shape; 64-bit
+    // arithmetic for larger grouped GEMMs)
+    int lo, hi;
+    if (units_e < (1 << 24) && grid <= 256) {
+      const uint32_t h = static_cast<uint32_t>(units_e), w = static_cast<uint32_t>(workers);
+      lo = static_cast<int>(static_cast<uint32_t>(j) * h / w);
+      hi = static_cast<int>(static_cast<uint32_t>(j + 1) * h / w);
+    } else {
+      lo = static_cast<int>(static_cast<long long>(j) * units_e / workers);
+      hi = static_cast<int>(static_cast<long long>(j + 1) * units_e / workers);
+    }
+    lo *= 2 / U;
+    hi *= 2 / U;
     r.h0 = 2 * pre_e + lo;
     r.h1 = 2 * pre_e + hi;
     r.s0 = pre_e + lo / 2;
@@ -664,41 +677,72 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     };
     // Stable ranks (route order = wave, chunk, lane, component): a segment's
     // routes in the chunks of the waves before mine are the sum of those
-    // waves' histogram rows; inside a chunk, one ballot per component gives
-    // the matches of every lane, so a lane's first rank is the count of
-    // matches in the lanes before it (mbcnt over the four masks) and the
-    // chunk's total is their popcount. Keep the ranks that fall in my strips.
+    // waves' histogram rows (q0). Inside my wave, each lane compares its four
+    // ids of every chunk with the segment (a 4-bit match mask per chunk) and
+    // one DPP scan of the per-lane match counts (two chunks per 32-bit word,
+    // 16-bit fields: at most 256 matches per chunk) gives every lane its
+    // rank base in each chunk. Only lanes with a match then loop over their
+    // set bits and keep the ranks that fall in my strips. (One scan per two
+    // chunks replaces four ballots and two mbcnts per chunk.)
+    constexpr int kPairs = (kIdChunks + 1) / 2;
 #pragma unroll 1
     for (int i = 0; i < nseg; ++i) {
       const Seg sg = seg_read(i);
       // (one LDS read per lane and a wave sum: a loop of dependent reads
       // costs one LDS round trip per earlier wave)
       const int32_t earlier = s_cntw[(lane < kWaves ? lane : 0) * 64 * nblk + sg.e];
-      int32_t q = wave_sum(lane < wave ? earlier : 0);
+      const int32_t q0 = wave_sum(lane < wave ? earlier : 0);
+      const int32_t mine = __builtin_amdgcn_readlane(earlier, wave);
+      if (q0 >= sg.hi || q0 + mine <= sg.lo) continue;  // no rank of this wave lies in my strips
+      static_assert(kIdChunks <= 16, "4 match bits per chunk in 64 bits");
+      uint64_t mk = 0;  // bit 4u + k: component k of chunk u matches
+      uint32_t packed[kPairs];
+#pragma unroll
+      for (int j = 0; j < kPairs; ++j) packed[j] = 0;
 #pragma unroll
       for (int u = 0; u < kIdChunks; ++u) {
-        if (c_begin + u < c_end && q < sg.hi) {
-          const int vals[4] = {idv[u].x, idv[u].y, idv[u].z, idv[u].w};
-          uint32_t before = 0;  // matches in the lanes below mine
-          int32_t chunk = 0;    // matches in the chunk
+        const uint32_t m = (idv[u].x == sg.e ? 1u : 0u) | (idv[u].y == sg.e ? 2u : 0u) |
+                           (idv[u].z == sg.e ? 4u : 0u) | (idv[u].w == sg.e ? 8u : 0u);
+        mk |= static_cast<uint64_t>(m) << (4 * u);
+        packed[u >> 1] += static_cast<uint32_t>(__builtin_popcount(m)) << (16 * (u & 1));
+      }
+      int32_t base[kIdChunks];
+      int32_t run = q0;
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint64_t mk = __ballot(vals[k] == sg.e);
-            before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mk >> 32),
-                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), before));
-            chunk += __builtin_popcountll(mk);
-          }
-          int rank = q + static_cast<int>(before);
-          const int r = (c_begin + u) * 256 + 4 * lane;
+      for (int j = 0; j < kPairs; ++j) {
+        if (c_begin + 2 * j < c_end) {
+          const uint32_t incl = static_cast<uint32_t>(rr::dev::wave_inclusive_scan(static_cast<int32_t>(packed[j])));
+          const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(incl), 63));
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            if (vals[k] == sg.e) {
-              if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = r + k;
-              ++rank;
+          for (int h = 0; h < 2; ++h) {
+            const int u = 2 * j + h;
+            if (u < kIdChunks) {
+              const int32_t inc = static_cast<int32_t>((incl >> (16 * h)) & 0xFFFFu);
+              const int32_t cnt = static_cast<int32_t>((packed[j] >> (16 * h)) & 0xFFFFu);
+              base[u] = run + inc - cnt;
+              run += static_cast<int32_t>((tot >> (16 * h)) & 0xFFFFu);
             }
           }
-          q += chunk;
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if (2 * j + h < kIdChunks) base[2 * j + h] = run;
+          }
         }
+      }
+      // lanes with matches: one trip per match (divergent; usually none or one)
+      uint64_t left = mk;
+      while (left != 0) {
+        const int bit = __builtin_ctzll(left);
+        left &= left - 1;
+        const int u = bit >> 2;
+        const int k = bit & 3;
+        int32_t b0 = base[0];
+#pragma unroll
+        for (int uu = 1; uu < kIdChunks; ++uu) b0 = u == uu ? base[uu] : b0;
+        const uint32_t m = static_cast<uint32_t>(mk >> (4 * u)) & 15u;
+        const int rank = b0 + __builtin_popcount(m & ((1u << k) - 1u));
+        if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = (c_begin + u) * 256 + 4 * lane + k;
       }
     }
     __syncthreads();
@@ -932,7 +976,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
           __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (kDeferred) {
-          if ((c & 3) == 3 && pending) epilogue_row(c >> 2, acc_prev, prev);
+          if (c < 4 && pending) epilogue_row(c, acc_prev, prev);
         }
       }
       }

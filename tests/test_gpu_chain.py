@@ -310,6 +310,9 @@ def run_stages(cfg, inp, device, ctx):
     # K = 256 with two-strip segments: workgroup ranges span up to three
     # segments (a later segment's B loaded ahead, the middle one on the switch)
     ("tokens", 4096, 256, 256, 128), ("tokens", 2048, 256, 256, 64),
+    # the merged launch's route limit (16384 routes held in registers): 16
+    # id chunks per wave with four waves (N <= 64), 8 with eight
+    ("tokens", 8192, 64, 256, 64), ("logits", 8192, 64, 128, 128),
 ])
 @pytest.mark.parametrize("with_inverse", [True, False])
 def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):

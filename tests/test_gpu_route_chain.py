@@ -209,7 +209,9 @@ def _same(a, b):
 
 
 @pytest.mark.parametrize("shape", [(512, 64, 2, 128, 128), (2048, 64, 8, 128, 128), (8192, 64, 8, 64, 64),
-                                   (333, 7, 4, 13, 9), (1000, 128, 4, 300, 40)])
+                                   (333, 7, 4, 13, 9), (1000, 128, 4, 300, 40),
+                                   # 16384 routes: the merged launch's limit, four waves
+                                   (4096, 64, 4, 128, 64)])
 @pytest.mark.parametrize("with_x_permuted", [True, False])
 def test_fused_route_chain_matches_stage_by_stage(ctx, device, shape, with_x_permuted):
     """The fused route chain (one merged launch + unpermute where the strip
