@@ -297,6 +297,37 @@ def test_histogram_large_paths(ctx, guarded, routes, experts, offset):
         assert counts.canaries_intact() and offsets.canaries_intact() and ids.canaries_intact()
 
 
+@pytest.mark.parametrize("experts,share,offset", [(33, 0.15, 0), (33, 0.5, 1), (1024, 0.95, 0), (256, 0.3, 2),
+                                                  (3, 0.2, 0)])
+def test_histogram_large_hot_expert(ctx, guarded, experts, share, offset):
+    """Multi-block path with a dominant expert at several shares (waves that
+    see it among their first ids count it with ballots instead of LDS
+    atomics; the rest count it by atomics), out-of-range ids in the mix, and
+    two calls in a row; counts and offsets exact, canaries intact."""
+    routes = 300007
+    rng = np.random.default_rng(experts + int(share * 100))
+    ids_h = rng.integers(0, experts, routes).astype(np.int32)
+    hot = int(rng.integers(0, experts))
+    ids_h[rng.random(routes) < share] = hot
+    ids_h[rng.integers(0, routes, 40)] = -1
+    ids_h[rng.integers(0, routes, 40)] = experts
+    valid = ids_h[(ids_h >= 0) & (ids_h < experts)]
+    e_c = np.bincount(valid, minlength=experts).astype(np.int32)
+    e_o = np.concatenate([[0], np.cumsum(e_c)]).astype(np.int32)
+    ids = guarded(routes, np.int32, ids_h, offset_elems=offset)
+    for _ in range(2):
+        counts = guarded(experts, np.int32, np.full(experts, 77, np.int32))
+        offsets = guarded(experts + 1, np.int32, np.full(experts + 1, -9, np.int32))
+        ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
+            expert_ids=ids.ptr, counts=counts.ptr, offsets=offsets.ptr, route_pairs=routes,
+            experts=experts, kernel=NATIVE), ctx))
+        assert np.array_equal(counts.read(), e_c) and np.array_equal(offsets.read(), e_o)
+        ok(rr.histogram(rr.HistogramArgs(expert_ids=ids.ptr, counts=counts.ptr, route_pairs=routes,
+                                         experts=experts, kernel=NATIVE), ctx))
+        assert np.array_equal(counts.read(), e_c)
+        assert counts.canaries_intact() and offsets.canaries_intact() and ids.canaries_intact()
+
+
 # -------------------------------------------------------------------- permute
 
 def run_permute(ctx, device, x_h, ids_h, experts, kernel, with_inverse=True, offset=0):
@@ -357,6 +388,9 @@ def test_permute_unaligned_duplicate_ids(ctx, device, kat, kernel):
     (2500, 64, 2, 1100), (1500, 300, 4, 1031), (17000, 8, 2, 1024),
     # ... few experts (ballot recount) with block prefixes that end mid-quad
     (3001, 16, 3, 1030), (4100, 5, 1, 1024),
+    # ... destination rows at every 16-byte phase across chunk boundaries
+    # (a chunk is 2048 floats: the realigned quads take the next chunk's first)
+    (700, 16, 2, 2049), (300, 8, 2, 4097), (257, 8, 2, 6143),
 ])
 def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     rng = np.random.default_rng(tokens + experts)
