@@ -10,6 +10,7 @@ Build with `make -C oracle` (also done by __graft_entry__.build()).
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
@@ -17,7 +18,8 @@ from pathlib import Path
 import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
-LIB_PATH = ORACLE_DIR / "liboracle.so"
+# RR_ORACLE_LIBRARY: another build of the oracle (tests/sanitize.sh's instrumented one)
+LIB_PATH = Path(os.environ.get("RR_ORACLE_LIBRARY") or ORACLE_DIR / "liboracle.so")
 
 RRO_OK = 0
 RRO_EINVAL = -1

@@ -13,6 +13,7 @@ handle (``torch.cuda.current_stream().cuda_stream``).
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import byref
 
 # One HIP runtime serves a process: the library binds whichever
@@ -63,7 +64,9 @@ from ._capi import (  # noqa: F401  (re-exported vocabulary)
     bind,
 )
 
-LIB_PATH = Path(__file__).resolve().parent / "libraggedroute_amd.so"
+# RR_LIBRARY names another build of the same library to load instead (the
+# host-sanitizer run of tests/sanitize.sh loads its instrumented build).
+LIB_PATH = Path(os.environ.get("RR_LIBRARY") or Path(__file__).resolve().parent / "libraggedroute_amd.so")
 
 
 def _load() -> ctypes.CDLL:

@@ -104,16 +104,6 @@ bool slurp(const char* path, std::string* text) {
   return !failed;
 }
 
-// Header line 4: exactly four integers.
-bool parse_shape(const std::string& line, int32_t (&v)[4]) {
-  Cursor c(line);
-  std::string w;
-  for (int32_t& x : v) {
-    if (!c.word(&w) || !parse_int32(w, &x)) return false;
-  }
-  return !c.word(&w);
-}
-
 void set_text(char* dst, std::size_t size, const std::string& src) noexcept {
   const std::size_t n = src.size() < size ? src.size() : size - 1;
   std::memcpy(dst, src.data(), n);
@@ -129,7 +119,7 @@ rr_status load(const char* path, int32_t want, rr_route_trace_info* info, int32_
   if (!slurp(path, &text)) return invalid_argument("route trace file cannot be opened or read");
   Cursor cur(std::move(text));
 
-  std::string tag, trace_id, kind, shape_line;
+  std::string tag, trace_id, kind;
   if (!cur.line(&tag) || tag != kSchemaTag) {
     return invalid_argument("route trace: line 1 must be raggedroute.route_trace.v1");
   }
@@ -139,9 +129,15 @@ rr_status load(const char* path, int32_t want, rr_route_trace_info* info, int32_
   if (!cur.line(&kind) || (kind != "production" && kind != "captured" && kind != "synthetic_fixture")) {
     return invalid_argument("route trace: line 3 names no known source kind");
   }
+  // The shape is the next four words, wherever the lines break (as the
+  // reference reads it with stream extraction); the first record may follow
+  // on the same line.
   int32_t shape[4] = {0, 0, 0, 0};
-  if (!cur.line(&shape_line) || !parse_shape(shape_line, shape)) {
-    return invalid_argument("route trace: line 4 must hold four integers T E top_k frames");
+  for (int32_t& v : shape) {
+    std::string w;
+    if (!cur.word(&w) || !parse_int32(w, &v)) {
+      return invalid_argument("route trace: the shape after line 3 must be four integers T E top_k frames");
+    }
   }
   const int32_t tokens = shape[0], experts = shape[1], top_k = shape[2], frames = shape[3];
   if (tokens < 1 || experts < 1 || experts > RR_MAX_EXPERTS || top_k < 1 || top_k > experts ||

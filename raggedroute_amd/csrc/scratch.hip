@@ -11,7 +11,10 @@
 // memset. Every call on one GPU shares that GPU's copy and leaves its
 // contents behind; no call relies on them (each writes the cursors and route
 // scratch it reads), so nothing needs clearing between calls, but calls that
-// overlap on one GPU (concurrent streams, threads) race on it.
+// overlap on one GPU (concurrent streams, threads) race on it. The address
+// lookup of a device's first call is no stream operation: that call may sit
+// inside a thread-local stream capture (the graph then replays the chain
+// with the resolved address).
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -65,8 +68,8 @@ rr_status scratch_address(void** out) noexcept {
 
 extern "C" rr_status rr_chain_from_tokens_noalloc(const rr_chain_args* args,
                                                   const rr_runtime_context* context) {
-  if (args == nullptr) return rr::invalid_argument("chain args must not be null");
-  if (context == nullptr) return rr::invalid_argument("runtime context must not be null");
+  if (args == nullptr) return rr::invalid_argument("rr_chain_from_tokens_noalloc: no argument struct was given");
+  if (context == nullptr) return rr::invalid_argument("no runtime context was given");
   // (checked before any device call)
   if (rr_chain_workspace_size(args) > rr::kScratchBytes) {
     return rr::invalid_argument(

@@ -57,9 +57,13 @@ GOOD = FIXTURE.read_text()
     (lambda s: s.replace("8 8 2 3", "8 1025 2 3"), "shape out of range"),
     (lambda s: s.replace("8 8 2 3", "8 8 9 3"), "shape out of range"),
     (lambda s: s.replace("8 8 2 3", "8 8 2 0"), "shape out of range"),
-    (lambda s: s.replace("8 8 2 3", "8 8 2"), "line 4"),
-    (lambda s: s.replace("8 8 2 3", "8 8 2 3 1"), "line 4"),
-    (lambda s: s.replace("8 8 2 3", "8 8 2 x"), "line 4"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2"), "four integers"),
+    # (a fifth word is the first frame's id, as in the reference's stream read)
+    (lambda s: s.replace("8 8 2 3", "8 8 2 3 1"), "non-integer"),
+    (lambda s: s.replace("8 8 2 3", "8 8 2 x"), "four integers"),
+    # a word is a whole decimal integer (the reference's stream extraction
+    # would read 2 and then take x as the next word): a deliberate difference
+    (lambda s: s.replace("balanced 0 1", "balanced 0 1x"), "non-integer"),
     (lambda s: s.replace("skewed", "balanced"), "share a frame id"),
     (lambda s: s.replace("skewed", "sk/ewed"), "frame id"),
     (lambda s: s.replace("balanced 0 1", "balanced 0 8"), "outside"),
@@ -77,6 +81,24 @@ def test_reader_rejects_planted_errors(tmp_path, mutate, message):
     assert bad != GOOD
     with pytest.raises(ValueError, match=message):
         route_trace.read(_write(tmp_path, bad), 0)
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda s: s.replace("8 8 2 3\n", "8 8\n2 3\n"),     # the shape over two lines
+    lambda s: s.replace("8 8 2 3\n", "8\n8\n2\n3\n"),  # one number a line
+    lambda s: s.replace("8 8 2 3\n", "8 8 2 3 "),        # the first record on line 4
+    lambda s: s.replace("\n", "\r\n"),                   # CRLF line ends
+])
+def test_reader_accepts_the_shape_wherever_lines_break(tmp_path, mutate):
+    """After the three header lines the shape is read as four words, as the
+    reference reads it with stream extraction (reference
+    include/raggedroute/benchmark/adapter_utils.h:276-281)."""
+    text = mutate(GOOD)
+    assert text != GOOD
+    for index in range(3):
+        got, want = route_trace.read(_write(tmp_path, text), index), route_trace.read(FIXTURE, index)
+        assert (got.frame_id, got.tokens, got.experts, got.top_k) == (want.frame_id, 8, 8, 2)
+        assert np.array_equal(got.ids, want.ids)
 
 
 def test_reader_accepts_layout_variants(tmp_path):

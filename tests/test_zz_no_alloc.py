@@ -6,11 +6,19 @@ each checked bit for bit against rr_chain_from_tokens with a caller
 workspace (every output poisoned before each call), on the merged two-launch
 plan (K <= 256) and on the three-launch plan (K > 256, whose route
 preparation keeps sorted_route in the scratch when the caller passes none).
+GPU, in a fresh process: the very first call on the device (which resolves
+the scratch address) made inside a thread-local stream capture, the graph
+replayed several times with the outputs poisoned between replays, every
+replay bit for bit equal to the eager rr_chain_from_tokens.
 CPU: shapes beyond the scratch are rejected before any device call.
 """
 from __future__ import annotations
 
+import subprocess
+import sys
+import textwrap
 from ctypes import byref
+from pathlib import Path
 
 import pytest
 import torch
@@ -78,6 +86,56 @@ def test_noalloc_chain_matches_workspace_chain(device, shapes):
         for key in ref:
             assert _same(got[key], ref[key]), f"{key} differs (T={t})"
         assert not torch.isnan(got["y"]).any()
+
+
+CAPTURE_CHILD = textwrap.dedent("""
+    import sys
+    from ctypes import byref
+    sys.path.insert(0, REPO)
+    import torch
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    sys.path.insert(0, REPO + "/tests")
+    from test_zz_no_alloc import _outputs, _args, _same
+    device = torch.device("cuda:0")
+    t, e, k, n = 4096, 64, 256, 128
+    cfg = workloads.ChainConfig("noalloc", t, e, k, n, from_tokens=True)
+    inp = workloads.chain_inputs_device(cfg, 0, device)
+    got = _outputs(t, e, k, n, device)
+    side = torch.cuda.Stream(device)
+    bare = rr.RuntimeContext(stream=side.cuda_stream, architecture=int(rr.DeviceArchitecture.kGfx950))
+    args = _args(inp, got, t, e, k, n)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="thread_local"):
+        status = rr.lib.rr_chain_from_tokens_noalloc(byref(args), byref(bare))
+    assert status.ok(), status.message
+    ref = _outputs(t, e, k, n, device)
+    ref_args = _args(inp, ref, t, e, k, n)
+    ws = torch.empty(rr.get_chain_workspace_size(ref_args) // 4, dtype=torch.int32, device=device)
+    ctx = rr.RuntimeContext(stream=torch.cuda.current_stream(device).cuda_stream, workspace=ws.data_ptr(),
+                            workspace_bytes=ws.numel() * 4, architecture=int(rr.DeviceArchitecture.kGfx950))
+    assert rr.chain_from_tokens(ref_args, ctx).ok()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        for v in got.values():
+            v.fill_(float("nan") if v.dtype == torch.float32 else -7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for key in ref:
+            assert _same(got[key], ref[key]), f"replay {replay}: {key} differs"
+    print("captured first call: 3 replays equal to the eager chain")
+""")
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_a_graph_capture():
+    repo = str(Path(__file__).resolve().parent.parent)
+    proc = subprocess.run([sys.executable, "-c", f"REPO = {repo!r}\n" + CAPTURE_CHILD],
+                          capture_output=True, text=True, timeout=240)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0, proc.stderr[-2000:]
 
 
 def test_noalloc_rejects_shapes_beyond_the_scratch():
