@@ -334,6 +334,41 @@ def test_fused_chain_matches_stage_by_stage(ctx, device, shape, with_inverse):
     check_chain(cfg, inp, fused)
 
 
+@pytest.mark.parametrize("distribution,tokens,experts,hidden,output", [
+    ("single_hot", 4096, 64, 256, 128), ("single_hot", 4096, 64, 256, 64), ("single_hot", 777, 16, 128, 96),
+    ("zipf", 4096, 64, 256, 128), ("round_robin", 4096, 64, 256, 128), ("duplicate_free_hot", 8192, 64, 256, 64),
+])
+def test_fused_chain_skewed_routing_matches_stage_by_stage(ctx, device, distribution, tokens, experts, hidden,
+                                                           output):
+    """chain_from_logits with logits that select skewed routings (every token
+    on experts 0 and 1; Zipf; round robin; one expert in every token): the
+    merged launch's dominant-expert counting gives the same counts, offsets,
+    route map and outputs, bit for bit, as the operators run one by one."""
+    t, e = tokens, experts
+    if distribution == "duplicate_free_hot":
+        rng = np.random.default_rng(5)
+        ids = np.stack([np.full(t, 3), (3 + 1 + rng.integers(0, e - 1, t)) % e], axis=1).astype(np.int32)
+    else:
+        ids = workloads.topk_route_ids(t, 2, e, distribution, seed=2)
+    logits = np.full((t, e), -8.0, np.float32)
+    logits[np.arange(t), ids[:, 0]] = 2.0
+    logits[np.arange(t), ids[:, 1]] = 1.0
+    cfg = workloads.ChainConfig("skew", t, e, hidden, output, from_tokens=False)
+    inp = workloads.chain_inputs(cfg, seed=4)
+    inp["logits"] = logits
+    run = ChainRun(cfg, inp, device)
+    fused = run.run(ctx)
+    fused["cursors"] = to_host(run.ws[:e])
+    assert np.array_equal(fused["ids"], ids)
+    ref = run_stages(cfg, inp, device, ctx)
+    for key in ("ids", "weights", "counts", "offsets", "route_pos", "sorted_route", "x_permuted", "y_permuted",
+                "y", "cursors"):
+        a, b = fused[key], ref[key]
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), f"{key} differs"
+    check_chain(cfg, inp, fused)
+
+
 @pytest.mark.parametrize("kind,hidden", [("tokens", 48), ("logits", 48), ("tokens", 260), ("logits", 260)])
 def test_fused_launches_one_by_one_equal_chain(ctx, device, kind, hidden):
     """rr_chain_fused_launch over every launch in order writes what one chain
