@@ -297,12 +297,20 @@ struct SlabLayout {
   __device__ static int wn0(int wave) { return wave * COLS; }
 };
 
-template <class S, bool VEC, int MODE, bool DMA>
+// Staging of the k slices: registers, or direct loads into LDS (whole
+// 32-deep slices and 16-byte rows), or direct loads at any row alignment and
+// any K (the last slice's chunks past K, and at the end of W past N, fixed up
+// in LDS).
+enum Staging : int { kRegisters = 0, kDirect = 1, kDirectAnyAlign = 2 };
+
+template <class S, bool VEC, int MODE, int DMA>
 __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams prm) {
   constexpr bool kGroupedRows = MODE == kGrouped || MODE == kChainGrouped;
   // slab layouts for tiles of at most 64 rows (the 128 x 128 tile, 2 x 2 waves)
   constexpr bool kSlabs = S::BM == 128 && S::BN == 128 && S::WM == 2 && S::WN == 2;
-  static_assert(!DMA || (kSlabs && S::BK == DmaLayout::kBK && VEC), "DMA staging: the 128 x 128 x 32 tile");
+  static_assert(DMA == kRegisters || (kSlabs && S::BK == DmaLayout::kBK && (VEC || DMA == kDirectAnyAlign)),
+                "DMA staging: the 128 x 128 x 32 tile");
+  static_assert(DMA != kDirectAnyAlign || MODE != kChainGrouped, "any-alignment staging: dense and grouped");
   constexpr int kStageFloats = DMA ? DmaLayout::kStageFloats : S::kStageFloats;
   extern __shared__ float lds[];
   float* stages = lds;                                                             // kStages
@@ -490,8 +498,65 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
           bsrc[p] = B + static_cast<std::size_t>(kl) * N + (n < N ? n : N - 4);
         }
         const std::size_t b_slice = static_cast<std::size_t>(D::kBK) * N;
-        // Slice kt -> LDS stage kt & 1 (every block, also past a short tile's
-        // rows: a branch here would split the slice's code and its waits).
+        // Any alignment (rows start at any 4-byte boundary; the 16-byte loads
+        // take them): slices before the last hold only k < K, and B quads
+        // that cross N read the next k row (in bounds) into columns that are
+        // never stored. The last slice's chunks are loaded from alast / blast:
+        // a chunk wholly past K from the row's start, then zeroed; an A chunk
+        // across K, and a B chunk across N in row K - 1 (which could end
+        // W), from the row's last whole quad, then shifted into place with
+        // zeros after the row's end. fix holds 4 bits per chunk (A chunk p at
+        // bit 4p, B chunk p at 16 + 4p): 0 = as loaded, else v + 1 for v
+        // leading floats kept.
+        uint32_t fix = 0;
+        // The last slice: each chunk's address built and its load issued at
+        // once (nothing of it stays live across the slices before).
+        auto issue_last = [&](float* As) {
+          float* Bs = As + D::kAFloats;
+          const int k_last = (nk - 1) * D::kBK;
+          // (the lane id passes an empty asm so that none of this is hoisted
+          // out of the tile loop and kept live across it)
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          fix = 0;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int q = 4 * p + wave;
+            const int r = 8 * q + (ln >> 3);
+            const int kc = (ln & 7) ^ D::swa(r);
+            const int k0 = k_last + 4 * kc;
+            const float* row = asrc[p] - 4 * kc;  // the row's start
+            int keep = 4;
+            int at = k0;
+            if (k0 >= K) {
+              at = 0;
+              keep = 0;
+            } else if (k0 + 4 > K) {
+              at = K - 4;
+              keep = K - k0;
+            }
+            if (keep < 4) fix |= static_cast<uint32_t>(keep + 1) << (4 * p);
+            __builtin_amdgcn_global_load_lds(row + at, As + q * D::kBlockFloats, 16, 0, 0);
+          }
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int q = 4 * p + wave;
+            const int kl = 2 * q + (ln >> 5);
+            const int k = k_last + kl;
+            const int n = n0 + 4 * ((ln & 31) ^ D::swb(kl));
+            const float* brow = B + static_cast<std::size_t>(k < K ? k : 0) * N;
+            int bkeep = 4;
+            int at = n < N ? n : N - 4;
+            if (k >= K) {
+              bkeep = 0;
+            } else if (k == K - 1 && n < N && n + 4 > N) {
+              at = N - 4;
+              bkeep = N - n;
+            }
+            if (bkeep < 4) fix |= static_cast<uint32_t>(bkeep + 1) << (16 + 4 * p);
+            __builtin_amdgcn_global_load_lds(brow + at, Bs + q * D::kBlockFloats, 16, 0, 0);
+          }
+        };
         auto issue = [&](int kt, float* As) {
           float* Bs = As + D::kAFloats;
 #pragma unroll
@@ -503,6 +568,30 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
           for (int p = 0; p < 4; ++p) {
             const int q = 4 * p + wave;
             __builtin_amdgcn_global_load_lds(bsrc[p] + kt * b_slice, Bs + q * D::kBlockFloats, 16, 0, 0);
+          }
+        };
+        // The last slice's chunk fix-ups, by the wave that loaded them, after
+        // its loads have landed and before the barrier that publishes them.
+        auto fixup = [&](float* As) {
+          float* Bs = As + D::kAFloats;
+          auto fix_chunk = [&](float* d, uint32_t code) {
+            if (code == 0) return;
+            const int keep = static_cast<int>(code) - 1;
+            const v4f v = *reinterpret_cast<const v4f*>(d);
+            v4f o;
+            o[0] = keep == 3 ? v[1] : keep == 2 ? v[2] : keep == 1 ? v[3] : 0.0F;
+            o[1] = keep == 3 ? v[2] : keep == 2 ? v[3] : 0.0F;
+            o[2] = keep == 3 ? v[3] : 0.0F;
+            o[3] = 0.0F;
+            *reinterpret_cast<v4f*>(d) = o;
+          };
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const int q = 4 * p + wave;
+            fix_chunk(As + q * D::kBlockFloats + 4 * ln, (fix >> (4 * p)) & 15u);
+            fix_chunk(Bs + q * D::kBlockFloats + 4 * ln, (fix >> (16 + 4 * p)) & 15u);
           }
         };
         // Operand addresses inside a stage. A: row r = wm0 + 16 i + li, k
@@ -527,7 +616,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         // which write the other stage, are never ordered before them.)
         // (restrict: the stage read and the stage loaded are disjoint, which
         // lets the compiler leave the reads after the loads unwaited)
-        auto multiply_dma = [&](int kt, const float* __restrict__ As, float* __restrict__ next) {
+        auto multiply_dma = [&](const float* __restrict__ As, float* __restrict__ next, auto iss) {
           const float* Bs = As + D::kAFloats;
           v4f af[2][TM];
           v4f bf[2][TN];
@@ -541,9 +630,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
             }
           };
           read(0);
-          // (the last slice loads itself again into the unused stage: no
-          // branch in the slice, whose waits then stay per operand)
-          issue(kt + 1 < nk ? kt + 1 : kt, next);
+          iss(next);
           read(1);
 #pragma unroll
           for (int h = 0; h < 2; ++h) mfma_steps<TM, TN>(acc, af[h], bf[h]);
@@ -578,7 +665,7 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         // Slice kt + 1 streams into the other stage while slice kt is
         // multiplied; the barrier after each slice (which waits for the wave's
         // own LDS loads first) makes it visible and frees the stage just read.
-        auto slice = [&](int kt, float* cur, float* next) {
+        auto slice = [&](int kt, float* cur, float* next, auto iss, bool fix_next) {
           // Wave priority alternates by slice parity. Two workgroups share each
           // CU and the matrix pipe favours the older one's waves: on a tie the
           // first workgroup ran its tiles 1.4x faster than the second, which then
@@ -589,18 +676,50 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
             __builtin_amdgcn_s_setprio(1);
           }
           if (writes_slice(kt)) store_xp(kt, cur);
-          multiply_dma(kt, cur, next);
+          multiply_dma(cur, next, iss);
           // (the MFMAs stay ahead of the wait: moved past it, they would idle
           // behind the loads of the next slice)
           __builtin_amdgcn_sched_barrier(0);
           __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of slice kt + 1
+          if (fix_next) fixup(next);
           __syncthreads();
         };
-        if (nk > 0) issue(0, stages);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-          slice(kt, stages + (kt & 1) * kStageFloats, stages + ((kt + 1) & 1) * kStageFloats);
+        auto stage_of = [&](int kt) { return stages + (kt & 1) * kStageFloats; };
+        if constexpr (DMA == kDirect) {
+          if (nk > 0) issue(0, stages);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+          __syncthreads();
+          for (int kt = 0; kt < nk; ++kt) {
+            // (the last slice loads itself again into the unused stage: no
+            // branch in the slice, whose waits then stay per operand)
+            slice(kt, stage_of(kt), stage_of(kt + 1),
+                  [&](float* nx) { issue(kt + 1 < nk ? kt + 1 : kt, nx); }, false);
+          }
+        } else if (nk > 0) {
+          // Slices before the last two issue the next slice; slice nk - 2
+          // issues the last one from the clamped addresses (fixed up once
+          // landed); the last slice issues nothing. (The last slice's
+          // addresses are built only in that branch, so that they are not
+          // live across the loop.)
+          if (nk == 1) {
+            issue_last(stages);
+          } else {
+            issue(0, stages);
+          }
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+          if (nk == 1) fixup(stages);
+          __syncthreads();
+          for (int kt = 0; kt < nk; ++kt) {
+            slice(kt, stage_of(kt), stage_of(kt + 1),
+                  [&](float* nx) {
+                    if (kt + 2 < nk) {
+                      issue(kt + 1, nx);
+                    } else if (kt + 2 == nk) {
+                      issue_last(nx);
+                    }
+                  },
+                  kt + 2 == nk);
+          }
         }
       } else {
         Stage<S, VEC> st;
@@ -740,7 +859,7 @@ hipError_t allow_full_lds(Kernel kernel) {
   return status;
 }
 
-template <class S, bool VEC, int MODE, bool DMA>
+template <class S, bool VEC, int MODE, int DMA>
 hipError_t launch_one(dim3 grid, std::size_t lds, const GemmParams& prm, hipStream_t stream) {
   const hipError_t attr = allow_full_lds(rr_gemm_mfma_kernel<S, VEC, MODE, DMA>);
   if (attr != hipSuccess) return attr;
@@ -756,6 +875,13 @@ bool registers_forced() {
   return v != nullptr && std::strcmp(v, "registers") == 0;
 }
 
+// RR_GEMM_STAGING=aligned keeps the direct loads to aligned shapes (the
+// register path then takes the others), for A/B runs.
+bool direct_any_disabled() {
+  const char* v = std::getenv("RR_GEMM_STAGING");
+  return v != nullptr && std::strcmp(v, "aligned") == 0;
+}
+
 template <class S, int MODE>
 hipError_t launch_gemm(const GemmParams& prm, long tile_bound, hipStream_t stream) {
   const bool vec = (prm.K % 4 == 0) && (prm.N % 4 == 0) && aligned16(prm.X) && aligned16(prm.W) &&
@@ -768,15 +894,22 @@ hipError_t launch_gemm(const GemmParams& prm, long tile_bound, hipStream_t strea
                            2 * static_cast<std::size_t>(S::BM) * sizeof(int32_t);
   const dim3 g(static_cast<unsigned>(grid));
   if constexpr (S::BM == 128 && S::BN == 128 && S::WM == 2 && S::WN == 2 && S::BK == DmaLayout::kBK) {
-    // whole 32-deep slices and 16-byte rows: direct LDS loads
-    if (vec && prm.K % DmaLayout::kBK == 0 && !registers_forced()) {
-      const std::size_t lds = S::kStages * DmaLayout::kStageFloats * sizeof(float) + meta;
-      return launch_one<S, true, MODE, true>(g, lds, prm, stream);
+    const std::size_t lds = S::kStages * DmaLayout::kStageFloats * sizeof(float) + meta;
+    if (!registers_forced()) {
+      // whole 32-deep slices and 16-byte rows: direct LDS loads
+      if (vec && prm.K % DmaLayout::kBK == 0) return launch_one<S, true, MODE, kDirect>(g, lds, prm, stream);
+      // other K, N or 4-byte row alignment (dense and grouped): direct loads
+      // with the last slice fixed up
+      if constexpr (MODE != kChainGrouped) {
+        if (prm.K >= DmaLayout::kBK && prm.N >= 4 && !direct_any_disabled()) {
+          return launch_one<S, false, MODE, kDirectAnyAlign>(g, lds, prm, stream);
+        }
+      }
     }
   }
   const std::size_t lds = S::kStages * S::kStageFloats * sizeof(float) + meta;
-  return vec ? launch_one<S, true, MODE, false>(g, lds, prm, stream)
-             : launch_one<S, false, MODE, false>(g, lds, prm, stream);
+  return vec ? launch_one<S, true, MODE, kRegisters>(g, lds, prm, stream)
+             : launch_one<S, false, MODE, kRegisters>(g, lds, prm, stream);
 }
 
 // 128x128, four 64x64 waves, BK 32: large problems (C4, C5 grouped). (BK 16,

@@ -6,8 +6,9 @@ each output in the same k order (16-wide k chunks in ascending order, one MFMA
 step per 4 k), so dense and grouped outputs must be bit-identical to the
 default dispatch, and within the accumulation-aware bound of the float64
 product. Shapes cover aligned (vector loads) and odd K / N or
-offset pointers (scalar loads), ragged and empty segments and the K tails of
-the 16- and 64-deep slices.
+offset pointers (scalar loads; for the large tile, direct loads at any
+alignment with the last slice fixed up in LDS), ragged and empty segments and
+the K tails of the 16-, 32- and 64-deep slices.
 """
 from __future__ import annotations
 
@@ -22,9 +23,11 @@ from test_gpu_ops import NATIVE, check_grouped, gemm_ok, ok, run_grouped
 pytestmark = pytest.mark.gpu
 
 # "large/registers": the large tile with register-staged slices where the
-# direct LDS loads (K a multiple of 32, 16-byte rows) would otherwise run
-TILES = ["large", "large/registers", "small", "medium", "narrow", "small256", "medium256",
-         "narrow256"]
+# direct LDS loads would otherwise run; "large/aligned": direct loads only for
+# whole 32-deep slices and 16-byte rows (register staging for the rest, which
+# the default large tile loads directly at any alignment)
+TILES = ["large", "large/registers", "large/aligned", "small", "medium", "narrow", "small256",
+         "medium256", "narrow256"]
 
 
 @pytest.fixture()
@@ -58,6 +61,13 @@ GROUPED = [
     ([257, 3, 128], 64, 260, 0),                       # two slices, three column tiles
     ([0, 300, 5, 1000, 0, 0, 77, 1], 128, 128, 0),  # strip K = 128 instance (8 chunks)
     ([0, 300, 5, 1000, 0, 0, 77, 1], 128, 64, 1),   # ... four-wave strips, offset pointers
+    # direct loads at any alignment: the last slice's A chunk across K (3 of 4
+    # floats kept) and B chunk across N in the last row of W (the last expert
+    # has rows), fixed up in LDS
+    ([5, 9, 70], 35, 19, 0),
+    ([10, 20, 30], 32, 13, 1),                        # one slice, odd N, offset pointers
+    ([33, 1, 64, 97], 4095, 21, 0),                   # long K with a 31-float last slice
+    ([64, 2, 0, 191], 4001, 9, 1),                    # K % 4 == 1, offset pointers
 ]
 
 
@@ -79,7 +89,8 @@ def test_grouped_tiles_bit_identical(ctx, device, tile_env, counts, k, n, offset
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 64, 256), (300, 128, 96), (500, 128, 244), (77, 40, 260),
-                                   (129, 17, 33), (4096, 64, 128), (700, 128, 128)])
+                                   (129, 17, 33), (4096, 64, 128), (700, 128, 128), (300, 19, 4095),
+                                   (64, 13, 35)])
 def test_dense_tiles_bit_identical(ctx, device, tile_env, m, n, k):
     import torch
     from conftest import to_dev, to_host
