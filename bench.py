@@ -78,6 +78,12 @@ def parse(argv=None):
                     help="runner mode: calls per sample (the sample is their span divided by the count)")
     ap.add_argument("--profile-once", action="store_true",
                     help="runner mode: warm up, then enqueue one call without timing and print nothing")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="phase times of the headline chain's expert launch, read from the instrumentation "
+                         "build (RR_LIBRARY=raggedroute_amd/libraggedroute_amd_stamps.so)")
+    ap.add_argument("--phase-stamps-out", default="",
+                    help="--phase-stamps: also save the launch's raw stamps (workgroups x 8 waves x slots, "
+                         "int64 .npy) to this file")
     return ap.parse_args(argv)
 
 
@@ -902,6 +908,94 @@ def profile(torch, device, case):
         print("profile: c5 done (30 chains, 30 x grouped_gemm)", flush=True)
 
 
+# ------------------------------------------------------------ phase stamps
+
+STAMP_SLOTS = 48   # per wave, as g_phase_stamps in strip.hip
+STAMP_BLOCKS = 1024
+STAMP_PHASES = [   # (slot, phase ending at that stamp)
+    (1, "route-id loads issued, LDS cleared"), (2, "barrier (ids arrive during it)"),
+    (3, "histogram of the ids"), (4, "barrier"), (5, "per-expert sums and scans"),
+    (6, "strip assignment"), (7, "strip table, first k chunks of B issued"),
+    (8, "stable ranks of the range's routes"), (9, "barrier"),
+    (10, "route map, rest of B issued")]
+
+
+def phase_stamps(torch, device, chains=80, out=""):
+    """Phase times of the headline chain's expert launch (the merged route
+    preparation + expert GEMM + combine) from the instrumentation build, whose
+    strip kernel writes the shader clock at each phase boundary of every wave
+    (slots in raggedroute_amd/csrc/strip.hip). Runs `chains` chains and reads
+    the stamps of the last launch; each wave's shader-clock rate comes from the
+    100 MHz clock read at its start and end. Prints a markdown summary and one
+    JSON line. The stamps and their stores perturb the launch: the chain time
+    printed is the instrumented one."""
+    import ctypes
+    import raggedroute_amd as rr
+    from raggedroute_amd import workloads
+    try:
+        read = rr.lib.rr_debug_phase_stamps
+    except AttributeError:
+        print("phase stamps: the loaded library has no stamps; run with "
+              "RR_LIBRARY=raggedroute_amd/libraggedroute_amd_stamps.so", file=sys.stderr)
+        return 2
+    read.restype = ctypes.c_int
+    read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    cfg = workloads.HEADLINE
+    ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
+    for _ in range(chains):
+        ch.chain()
+    torch.cuda.synchronize()
+    means = batch_means(torch, ch.chain, samples=10, repeats=10)
+    torch.cuda.synchronize()
+    buf = np.zeros(STAMP_BLOCKS * 8 * STAMP_SLOTS, np.uint64)
+    assert read(buf.ctypes.data, buf.nbytes) == 0, "stamp copy failed"
+    st = buf.reshape(STAMP_BLOCKS, 8, STAMP_SLOTS).astype(np.int64)
+    st = st[st[:, 0, 39] > 0]  # the launch's workgroups (the array starts zeroed)
+    grid = st.shape[0]
+    if out:
+        np.save(out, st)
+    # each wave's shader-clock rate (cycles per us) from its 100 MHz clock reads
+    rate = (st[:, :, 37] - st[:, :, 0]) / np.maximum(1, st[:, :, 39] - st[:, :, 38]) * 100.0
+    us = (st - st[:, :, :1]) / rate[:, :, None]
+    strips = st[:, 0, 40]
+    halves = st[:, 0, 41]
+    total = us[:, :, 37].max(axis=1)
+    busy = total >= np.percentile(total, 90)
+    rows = []
+    prev = 0
+    for slot, name in STAMP_PHASES:
+        d = us[:, 0, slot] - us[:, 0, prev]
+        rows.append({"phase": name, "wave0_median_us": round(float(np.median(d)), 3),
+                     "wave0_busiest_median_us": round(float(np.median(d[busy])), 3)})
+        prev = slot
+    strip_rows = []
+    for k in range(3):
+        have = strips > k
+        if not have.any():
+            continue
+        top, past, done = 11 + 4 * k, 13 + 4 * k, 14 + 4 * k
+        for w in (0, 7):
+            strip_rows.append({"strip": k, "wave": w,
+                               "start_us": round(float(np.median(us[have, w, top])), 3),
+                               "top_to_barrier_us": round(float(np.median(us[have, w, past] - us[have, w, top])), 3),
+                               "mfma_us": round(float(np.median(us[have, w, done] - us[have, w, past])), 3)})
+    tail = us[:, 0, 37] - us[:, 0, 36]
+    rec = {"what": "phase stamps of the headline expert launch (instrumentation build)",
+           "chain_us_instrumented": round(statistics.median(means) * 1e6, 2),
+           "grid": grid, "strips_per_workgroup": np.bincount(strips).tolist(),
+           "half_strips_per_workgroup": np.bincount(halves).tolist(),
+           "shader_clock_ghz_median": round(float(np.median(rate)) / 1000.0, 3),
+           "workgroup_span_us": {"median": round(float(np.median(total)), 2), "max": round(float(total.max()), 2)},
+           "prologue": rows, "strips": strip_rows,
+           "last_epilogue_to_memory_done_us": round(float(np.median(tail)), 3)}
+    print("| phase (wave 0) | median us | busiest 10 % median us |")
+    print("|---|---|---|")
+    for r in rows:
+        print(f"| {r['phase']} | {r['wave0_median_us']} | {r['wave0_busiest_median_us']} |")
+    print(json.dumps(rec))
+    return 0
+
+
 # ------------------------------------------------------------ runner mode
 
 RUNNER_DEFAULTS = {"T": 4096, "E": 64, "K": 256, "N": 128, "top_k": 2, "distribution": "uniform",
@@ -1098,6 +1192,8 @@ def main() -> int:
     if args.profile:
         profile(torch, device, args.profile)
         return 0
+    if args.phase_stamps:
+        return phase_stamps(torch, device, out=args.phase_stamps_out)
     args.warmup = 20 if args.warmup is None else args.warmup
     cfg, ch, inputs, head = headline(torch, device, args)
     tokens_per_s = cfg.tokens / head["p50_s"]

@@ -7,6 +7,11 @@ that it travels with the repository snapshot.
 
     python raggedroute_amd/build.py          # full rebuild
 
+The same build also links libraggedroute_amd_stamps.so, an instrumentation
+copy whose strip.hip is compiled with -DRR_PHASE_STAMPS (phase stamps of the
+chain launch, read by `bench.py --phase-stamps`); nothing loads it unless
+RR_LIBRARY names it.
+
 Run it as a script (or load it by path): importing the package loads the
 library, which does not exist yet on a fresh checkout.
 """
@@ -28,6 +33,10 @@ INCLUDE = REPO / "include"
 BUILD = REPO / "_build"
 LIB_NAME = "libraggedroute_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+STAMPS_PATH = PKG_DIR / "libraggedroute_amd_stamps.so"
+# sources compiled a second time, with this define, for the instrumentation copy
+STAMPED_SOURCES = ("strip.hip",)
+STAMPS_DEFINE = "-DRR_PHASE_STAMPS"
 # Source revision and toolchain of the last build (git-ignored like the
 # library, and shipped beside it): benchmark records name what they ran.
 BUILD_INFO = PKG_DIR / "build_info.json"
@@ -66,11 +75,12 @@ def _run(cmd: list[str]) -> None:
         )
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.name + ".o")
+def _compile(src: Path, stamps: bool = False) -> Path:
+    obj = BUILD / (src.name + (".stamps.o" if stamps else ".o"))
     includes = [f"-I{INCLUDE}", f"-I{CSRC}"]
     if src.suffix == ".hip":
-        cmd = [_hipcc(), *HIP_FLAGS, *includes, "-c", str(src), "-o", str(obj)]
+        extra = [STAMPS_DEFINE] if stamps else []
+        cmd = [_hipcc(), *HIP_FLAGS, *extra, *includes, "-c", str(src), "-o", str(obj)]
     else:
         cmd = ["g++", *CXX_FLAGS, *includes, f"-I{ROCM / 'include'}", "-c", str(src), "-o", str(obj)]
     _run(cmd)
@@ -94,23 +104,33 @@ def _build_info() -> dict:
             "hip": version, "arch": ARCH, "hip_flags": " ".join(HIP_FLAGS)}
 
 
+def _link(objects: list[Path], out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    _run([_hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp),
+          *map(str, objects), f"-L{ROCM / 'lib'}", "-lamdhip64",
+          f"-Wl,-rpath,{ROCM / 'lib'}"])
+    shutil.move(str(tmp), str(out))
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source and link the shared library (and its phase-stamp
+    instrumentation copy); returns the library's path."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no sources under {CSRC}")
+    stamped = [src for src in sources if src.name in STAMPED_SOURCES]
     jobs = jobs or min(8, os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(_compile, sources))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    _run([_hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp),
-          *map(str, objects), f"-L{ROCM / 'lib'}", "-lamdhip64",
-          f"-Wl,-rpath,{ROCM / 'lib'}"])
-    shutil.move(str(tmp), str(LIB_PATH))
+        futures = [pool.submit(_compile, src) for src in sources]
+        stamp_futures = {src.name: pool.submit(_compile, src, True) for src in stamped}
+        objects = [f.result() for f in futures]
+        stamp_objects = {name: f.result() for name, f in stamp_futures.items()}
+    _link(objects, LIB_PATH)
+    _link([stamp_objects.get(src.name, obj) for src, obj in zip(sources, objects)], STAMPS_PATH)
     BUILD_INFO.write_text(json.dumps(_build_info(), indent=1) + "\n")
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} (and {STAMPS_PATH.name})")
     return LIB_PATH
 
 

@@ -52,6 +52,39 @@
 namespace rr::kern {
 namespace {
 
+// Phase stamps of the chain launch (instrumentation build only: strip.hip
+// compiled with -DRR_PHASE_STAMPS into libraggedroute_amd_stamps.so; the
+// product library has none of this). Lane 0 of every wave writes the shader
+// clock (s_memtime) at each phase boundary of the chain-mode kernel into
+// g_phase_stamps[(block * 8 + wave) * kStampSlots + i], with the 100 MHz
+// clock (s_memrealtime) at the start and end of the wave so that the shader
+// clock's rate can be read off each wave. Slots: 0 start; 1 / 2 around the
+// barrier after the id loads and LDS clears; 3 / 4 around the barrier after
+// the histogram; 5 before the strip assignment, 6 after it; 7 strip table and
+// the early part of B issued; 8 / 9 around the barrier after the rank passes;
+// 10 route map and the rest of B issued; per strip k < 6: 11 + 4k top,
+// 12 + 4k A rows stored, 13 + 4k past the barrier, 14 + 4k MFMAs issued; 36
+// last epilogue issued; 37 every memory operation done; 38 / 39 the 100 MHz
+// clock at start / end; 40 strips of the range; 41 half strips of the range.
+#ifdef RR_PHASE_STAMPS
+constexpr int kStampSlots = 48;
+constexpr int kStampBlocks = 1024;
+__device__ unsigned long long g_phase_stamps[kStampBlocks * 8 * kStampSlots];
+#define RR_STAMP_AT(i, value)                                                             \
+  do {                                                                                    \
+    if constexpr (MODE == kStripChain) {                                                  \
+      const unsigned long long v_ = (value);                                              \
+      if (lane == 0 && b < kStampBlocks) g_phase_stamps[(b * 8 + wave) * kStampSlots + (i)] = v_; \
+    }                                                                                     \
+  } while (0)
+#define RR_STAMP(i) RR_STAMP_AT(i, __builtin_amdgcn_s_memtime())
+#else
+#define RR_STAMP_AT(i, value) \
+  do {                        \
+  } while (0)
+#define RR_STAMP(i) RR_STAMP_AT(i, 0)
+#endif
+
 using rr::dev::lane_id;
 using rr::dev::lanemask_lt;
 
@@ -391,6 +424,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   // Consecutive workers on one XCD: the workgroups of one segment share its
   // weights through the same L2.
   const int worker = (grid % kXcds == 0) ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
+  RR_STAMP_AT(38, __builtin_amdgcn_s_memrealtime());
+  RR_STAMP(0);
 
   // ---- B of a segment: this wave's 16 columns, whole K, in registers ----
   // bq[c][s] = B[16c + 4g + s][16 wave + li]: sixteen lanes read 64
@@ -523,7 +558,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       hot0 = ok0 ? c0 : (ok1 ? c1 : -1);
       hot1 = ok0 && ok1 ? c1 : -1;
     }
+    RR_STAMP(1);
     __syncthreads();  // counts zeroed
+    RR_STAMP(2);
     int32_t* my_row = s_cntw + wave * 64 * nblk;  // this wave's own row
     auto unplaced = [&](int r) {
       // a route whose id lies outside [0, E) is never placed: its map entry
@@ -572,7 +609,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         }
       }
     }
+    RR_STAMP(3);
     __syncthreads();
+    RR_STAMP(4);
     // every wave sums the waves' rows itself (no combined row, no second barrier)
 #pragma unroll
     for (int j = 0; j < kMaxBlocks; ++j) {
@@ -622,6 +661,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     }
   }
 
+  RR_STAMP(5);
   const int total = tab.total_strips;
   StripRange range;
   if constexpr (kSingle) {
@@ -630,6 +670,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     range = assign_strips<kWaves == 8 ? 2 : 1>(tab, nblk, E, total, grid, worker,
                                                MODE == kStripChain ? p.max_strips : INT_MAX);
   }
+  RR_STAMP(6);
   const int s0 = range.s0;
   const int s1 = range.s1;
   // Half strips: waves [0, kWaves / 2) compute the left half of a strip's
@@ -683,6 +724,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
     }
   };
 
+  RR_STAMP(7);
   // ------------------------------------------- chain: routes of my strips
   float w_pending = 0.0F;
   if constexpr (MODE == kStripChain) {
@@ -798,7 +840,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         if (rank >= sg.lo && rank < sg.hi) s_slot[sg.base + rank] = (c_begin + u) * 256 + 4 * lane + k;
       }
     }
+    RR_STAMP(8);
     __syncthreads();
+    RR_STAMP(9);
   }
 
   // ------------------------------------------------------------ strip loop
@@ -929,8 +973,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
   } else {
     if (s0 < s1) load_b(cur.e);
   }
+  RR_STAMP(10);
   for (int s = s0; s < s1; ++s) {
     const StripInfo si = cur;
+    if (s - s0 < 6) RR_STAMP(11 + 4 * (s - s0));
     // No barrier before the A store: buffer s & 1 was last read by strip
     // s - 2's MFMAs, which every wave finished before the barrier below in
     // strip s - 1 (and the router's logit tile is rewritten only after that
@@ -955,7 +1001,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       }
       if (s == s0 && tid < (s1 - s0) * kRows) s_w[tid] = w_pending;
     }
+    if (s - s0 < 6) RR_STAMP(12 + 4 * (s - s0));
     __syncthreads();
+    if (s - s0 < 6) RR_STAMP(13 + 4 * (s - s0));
     // ---- prefetch the next strip's A rows (B of a new segment follows the
     // MFMAs, which still read this segment's B) ----
     if (s + 1 < s1) {
@@ -1040,6 +1088,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
         for (int r = 0; r < 4; ++r) epilogue_row(r, acc_prev, prev);
       }
     }
+    if (s - s0 < 6) RR_STAMP(14 + 4 * (s - s0));
     if (s + 1 < s1 && cur.e != si.e) {  // the next strip's segment
       if (kPfB && pf_e == cur.e) {
 #pragma unroll
@@ -1134,6 +1183,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void rr_strip_gemm_kernel(StripParam
       for (int r = 0; r < 4; ++r) epilogue_row(r, acc_prev, prev);
     }
   }
+#ifdef RR_PHASE_STAMPS
+  if constexpr (MODE == kStripChain) {
+    RR_STAMP(36);
+    __builtin_amdgcn_s_waitcnt(0);
+    RR_STAMP(37);
+    RR_STAMP_AT(39, __builtin_amdgcn_s_memrealtime());
+    RR_STAMP_AT(40, static_cast<unsigned long long>(s1 - s0));
+    RR_STAMP_AT(41, static_cast<unsigned long long>(range.h1 - range.h0));
+  }
+#endif
 }
 
 constexpr int kMaxDevices = 64;
@@ -1319,4 +1378,14 @@ hipError_t strip_chain(const float* x, const float* expert_weights, const int32_
   return launch_strip<kStripChain>(p, grid, stream);
 }
 
+#ifdef RR_PHASE_STAMPS
+// Instrumentation build only: copies the phase stamps of the last chain-mode
+// strip launch (kStampBlocks x 8 waves x kStampSlots 64-bit words) to host
+// memory; returns the hipError_t of the copy.
+extern "C" int rr_debug_phase_stamps(void* dst, size_t bytes) {
+  const size_t size = sizeof(g_phase_stamps);
+  return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_phase_stamps), bytes < size ? bytes : size, 0,
+                                              hipMemcpyDeviceToHost));
+}
+#endif
 }  // namespace rr::kern
