@@ -890,7 +890,9 @@ def profile(torch, device, case):
         print("profile: headline done (50 chains, 20 x each fused launch, 20 x each stage)", flush=True)
     elif case == "c4":
         c4(torch, device, reps=2, samples=3)
-        print("profile: c4 done", flush=True)
+        print("profile: c4 (K 4096, N 14336) done", flush=True)
+        c4(torch, device, hidden=4095, output=14335, reps=2, samples=3)
+        print("profile: c4 (K 4095, N 14335) done", flush=True)
     elif case == "c3":
         c3(torch, device)
         print("profile: c3 done", flush=True)
