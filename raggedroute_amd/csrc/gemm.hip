@@ -501,13 +501,13 @@ __global__ __launch_bounds__(S::kThreads, 2) void rr_gemm_mfma_kernel(GemmParams
         // Any alignment (rows start at any 4-byte boundary; the 16-byte loads
         // take them): slices before the last hold only k < K, and B quads
         // that cross N read the next k row (in bounds) into columns that are
-        // never stored. The last slice's chunks are loaded from alast / blast:
-        // a chunk wholly past K from the row's start, then zeroed; an A chunk
-        // across K, and a B chunk across N in row K - 1 (which could end
-        // W), from the row's last whole quad, then shifted into place with
-        // zeros after the row's end. fix holds 4 bits per chunk (A chunk p at
-        // bit 4p, B chunk p at 16 + 4p): 0 = as loaded, else v + 1 for v
-        // leading floats kept.
+        // never stored. issue_last loads the last slice: a chunk wholly past
+        // K from an in-bounds address (the A row's start, B's row 0), then
+        // zeroed; an A chunk across K, and a B chunk across N in row K - 1
+        // (which could end W), from the row's last whole quad, then shifted
+        // into place with zeros after the row's end. fix holds 4 bits per
+        // chunk (A chunk p at bit 4p, B chunk p at 16 + 4p): 0 = as loaded,
+        // else v + 1 for v leading floats kept.
         uint32_t fix = 0;
         // The last slice: each chunk's address built and its load issued at
         // once (nothing of it stays live across the slices before).
