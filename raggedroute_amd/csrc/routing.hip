@@ -23,6 +23,7 @@ using rr::dev::lane_id;
 using rr::dev::lanemask_lt;
 using rr::dev::match_mask;
 using rr::dev::wave_inclusive_scan;
+using rr::dev::wave_lds_sync;
 
 constexpr int kBlock = 1024;  // 16 waves
 constexpr int kWavesPerBlock = kBlock / 64;
@@ -828,9 +829,37 @@ __global__ __launch_bounds__(256) void rr_permute_rows_kernel(const float* __res
 // their tokens' rows. The rank phase runs under the first loads' latency and
 // the copy waits for no second launch. The recount reads the routes before a
 // block's range, so the host keeps this kernel to R <= kFusedRankRoutes.
+//
+// REALIGN (rows that do not start on a 128-byte line: hidden % 32 != 0 or an
+// offset base pointer): a wave reads its row as whole 16-byte quads from the
+// 128-byte line that holds the row's first float, kRealignPad quads of margin
+// on either side of each 512-quad chunk, into its own LDS strip; every
+// destination row is then written as 16-byte quads counted from ITS first
+// 128-byte line, each lane gathering its four floats from the strip at the
+// source-destination phase difference. A wave's store instruction then covers
+// whole 128-byte lines (only a row's first and last line are partial), where
+// quads at the row's own offset split each line between two store
+// instructions. Measured on an isolated copy of C4's shape (T = 8192, two
+// destinations per token, stable destinations, 16 KB rows): K = 4095 82-83 us
+// (0.61 of HBM) against 86-88 us at the row's offset, K = 4093 84 against 87;
+// K = 4096 (aligned rows) 84 against 80, so aligned rows keep the plain quads.
+// This kernel at C4 K = 4095, cold: 92.1 us before, 87.9 with the strip, 86.9
+// with the next chunk's loads issued before the current chunk's stores.
+// The loads read at most the 128-byte lines that hold a row's first and last
+// float (never a line without a float of x), and the stores write only the
+// row's own floats.
 constexpr int kFusedRankRoutes = 32768;
 constexpr int kFusedWaves = 4;
+constexpr int kRealignPad = 8;                                                  // quads
+constexpr int kRealignStripQuads = 64 * kRowQuadsInFlight + 2 * kRealignPad;  // per wave
+typedef float f4a __attribute__((ext_vector_type(4)));                         // 16-byte aligned
 
+__host__ __device__ inline int realign_strip_offset(int experts, int tokens_per_block, int top_k) {
+  // int32 offset of the realign strips in the block's LDS, 16-byte aligned
+  return ((kFusedWaves + 1) * experts + tokens_per_block * top_k + 3) & ~3;
+}
+
+template <bool REALIGN>
 __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
     const float* __restrict__ x, const int32_t* __restrict__ ids, const int32_t* __restrict__ offsets,
     int32_t* cursors, float* __restrict__ x_permuted, int32_t* __restrict__ route_pos,
@@ -851,6 +880,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
   const int end = t_end * top_k;
   const int cols = static_cast<int>(quads_of(hidden));
 
+  constexpr int kChunk = 64 * kRowQuadsInFlight;  // quads per chunk
   f4u v[kRowQuadsInFlight];
   auto load_chunk = [&](const float* src, int q0) {
 #pragma unroll
@@ -864,10 +894,39 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
       }
     }
   };
+  // REALIGN: quads [c0, c0 + kChunk) of the row's lines (nq quads from line0)
+  // into v, and lanes 0..2 kRealignPad-1 the margin quads c0 - kRealignPad ..
+  // c0 - 1 and c0 + kChunk .. c0 + kChunk + kRealignPad - 1 into `edge`.
+  f4a edge = f4a{0.0F, 0.0F, 0.0F, 0.0F};
+  auto load_lines = [&](const f4a* line0, int nq, int c0) {
+#pragma unroll
+    for (int u = 0; u < kRowQuadsInFlight; ++u) {
+      const int q = c0 + lane + 64 * u;
+      if (q < nq) {
+        const f4a w = __builtin_nontemporal_load(line0 + q);
+        v[u] = f4u{w.x, w.y, w.z, w.w};
+      } else {
+        v[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
+      }
+    }
+    const int eq = lane < kRealignPad ? c0 - kRealignPad + lane : c0 + kChunk + lane - kRealignPad;
+    edge = f4a{0.0F, 0.0F, 0.0F, 0.0F};
+    if (lane < 2 * kRealignPad && eq >= 0 && eq < nq) edge = __builtin_nontemporal_load(line0 + eq);
+  };
+  auto row_phase = [](const float* row) {  // floats from the row's 128-byte line to the row
+    return static_cast<int>((reinterpret_cast<uintptr_t>(row) >> 2) & 31);
+  };
   // The first row's first chunk stays in flight while the block ranks.
   const int t_first = t_begin + wave;
-  constexpr int kChunk = 64 * kRowQuadsInFlight;  // quads per chunk
-  if (t_first < t_end) load_chunk(x + static_cast<std::size_t>(t_first) * hidden, 0);
+  if (t_first < t_end) {
+    const float* src = x + static_cast<std::size_t>(t_first) * hidden;
+    if constexpr (REALIGN) {
+      const int hs = row_phase(src);
+      load_lines(reinterpret_cast<const f4a*>(src - hs), (hidden + hs + 3) >> 2, 0);
+    } else {
+      load_chunk(src, 0);
+    }
+  }
 
   // ---- rank phase (block-wide) ----
   for (int i = tid; i < kFusedWaves * experts; i += kThreads) wc[i] = 0;
@@ -972,6 +1031,76 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
   }
 
   // ---- copy phase: wave w copies rows t_begin + w, + waves, ... ----
+  if constexpr (REALIGN) {
+    f4a* strip = reinterpret_cast<f4a*>(lds + realign_strip_offset(experts, tokens_per_block, top_k)) +
+                 wave * kRealignStripQuads;
+    const float* strip_f = reinterpret_cast<const float*>(strip);
+    // Once a chunk sits in the strip its registers are free: the next chunk's
+    // loads (this row's next or the wave's next row's first) are issued before
+    // the current chunk's stores, so their latency runs under the stores.
+    auto span_of = [&](int t, int nq) {  // quads to cover: the source's and every destination's
+      const int32_t* my_slots = slot + (t - t_begin) * top_k;
+      int span = nq;
+      for (int j = 0; j < top_k; ++j) {
+        const int32_t pos = my_slots[j];
+        if (pos >= 0) {
+          const int nd = (hidden + row_phase(x_permuted + static_cast<std::size_t>(pos) * hidden) + 3) >> 2;
+          span = nd > span ? nd : span;
+        }
+      }
+      return span;
+    };
+    for (int t = t_first; t < t_end; t += kFusedWaves) {
+      const float* src = x + static_cast<std::size_t>(t) * hidden;
+      const int hs = row_phase(src);
+      const f4a* line0 = reinterpret_cast<const f4a*>(src - hs);
+      const int nq = (hidden + hs + 3) >> 2;
+      const int32_t* my_slots = slot + (t - t_begin) * top_k;
+      const int span = span_of(t, nq);
+      for (int c0 = 0; c0 < span; c0 += kChunk) {
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) {
+          strip[kRealignPad + lane + 64 * u] = f4a{v[u].x, v[u].y, v[u].z, v[u].w};
+        }
+        if (lane < 2 * kRealignPad) strip[lane < kRealignPad ? lane : kChunk + lane] = edge;
+        wave_lds_sync();
+        if (c0 + kChunk < span) {
+          load_lines(line0, nq, c0 + kChunk);
+        } else if (t + kFusedWaves < t_end) {
+          const float* next = src + static_cast<std::size_t>(kFusedWaves) * hidden;
+          const int hn = row_phase(next);
+          load_lines(reinterpret_cast<const f4a*>(next - hn), (hidden + hn + 3) >> 2, 0);
+        }
+        for (int j = 0; j < top_k; ++j) {
+          const int32_t pos = my_slots[j];  // (one LDS address: a broadcast)
+          if (pos < 0) continue;            // wave-uniform
+          float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden;
+          const int hd = row_phase(dst);
+          float* dline = dst - hd;
+          const int nd = (hidden + hd + 3) >> 2;
+#pragma unroll
+          for (int u = 0; u < kRowQuadsInFlight; ++u) {
+            const int i = c0 + lane + 64 * u;  // destination quad, from dline
+            if (i < nd) {
+              // floats 4 i - hd .. +3 of the row = strip floats from the chunk's margin
+              const int off = 4 * (kRealignPad + lane + 64 * u) + hs - hd;
+              const f4a o = f4a{strip_f[off], strip_f[off + 1], strip_f[off + 2], strip_f[off + 3]};
+              const int f0 = 4 * i - hd;
+              if (f0 >= 0 && f0 + 4 <= hidden) {
+                __builtin_nontemporal_store(o, reinterpret_cast<f4a*>(dline + 4 * i));
+              } else {
+                for (int e = 0; e < 4; ++e) {
+                  if (f0 + e >= 0 && f0 + e < hidden) dst[f0 + e] = o[e];
+                }
+              }
+            }
+          }
+        }
+        wave_lds_sync();  // the strip's reads before the next chunk's writes
+      }
+    }
+    return;
+  }
   for (int t = t_first; t < t_end; t += kFusedWaves) {
     const float* src = x + static_cast<std::size_t>(t) * hidden;
     const int32_t* my_slots = slot + (t - t_begin) * top_k;
@@ -1196,12 +1325,24 @@ hipError_t token_permute_stable(const float* x, const int32_t* ids, const int32_
     const int grid = tokens < 1024 ? tokens : 1024;
     const int tpb = (tokens + grid - 1) / grid;
     const int blocks = (tokens + tpb - 1) / tpb;
-    const std::size_t lds =
-        (static_cast<std::size_t>(kFusedWaves + 1) * experts + static_cast<std::size_t>(tpb) * top_k) *
-        sizeof(int32_t);
-    rr_permute_rank_rows_kernel<<<blocks, kFusedWaves * 64, lds, stream>>>(
-        x, ids, offsets, cursors, x_permuted, route_pos, sorted_route, tokens, top_k, hidden, experts,
-        bits_for(experts), tpb);
+    const bool lines = hidden % 32 == 0 && reinterpret_cast<uintptr_t>(x) % 128 == 0 &&
+                       reinterpret_cast<uintptr_t>(x_permuted) % 128 == 0;
+    if (lines) {
+      const std::size_t lds =
+          (static_cast<std::size_t>(kFusedWaves + 1) * experts + static_cast<std::size_t>(tpb) * top_k) *
+          sizeof(int32_t);
+      rr_permute_rank_rows_kernel<false><<<blocks, kFusedWaves * 64, lds, stream>>>(
+          x, ids, offsets, cursors, x_permuted, route_pos, sorted_route, tokens, top_k, hidden, experts,
+          bits_for(experts), tpb);
+    } else {
+      // top_k <= E <= 1024 (the entry's checks) and tpb * top_k <= 32 + top_k: under 59 KB
+      const std::size_t lds = static_cast<std::size_t>(realign_strip_offset(experts, tpb, top_k)) * sizeof(int32_t) +
+                              static_cast<std::size_t>(kFusedWaves) * kRealignStripQuads * sizeof(f4a);
+      if (lds > 64 * 1024) return hipErrorInvalidValue;
+      rr_permute_rank_rows_kernel<true><<<blocks, kFusedWaves * 64, lds, stream>>>(
+          x, ids, offsets, cursors, x_permuted, route_pos, sorted_route, tokens, top_k, hidden, experts,
+          bits_for(experts), tpb);
+    }
     return hipGetLastError();
   }
   // One sub-chunk per block up to 64 blocks; beyond that the chunk grows so the

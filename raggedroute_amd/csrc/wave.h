@@ -15,6 +15,15 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return (uint64_t{1} << lane_id()) - 1;  // lane 0 -> 0
 }
 
+// Orders one wave's LDS accesses on either side of it for the compiler. The
+// hardware already runs a wave's LDS instructions in issue order, so a lane's
+// read after this sees what other lanes of the same wave wrote before it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Mask of the active lanes whose `key` equals this lane's key, for keys in
 // [0, 2^bits). `bits` ballots replace a match-any instruction (CDNA has none).
 __device__ __forceinline__ uint64_t match_mask(uint32_t key, int bits, uint64_t active) {

@@ -408,6 +408,25 @@ def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     assert np.array_equal(cursors, np.diff(offsets))
 
 
+@pytest.mark.parametrize("tokens,experts,top_k,hidden,offset", [
+    # rows whose width is a multiple of 32 floats but whose base pointers sit
+    # 4, 28 or 124 bytes past a 128-byte line: every row is copied through the
+    # line-realigned path; with a tail, a 2-chunk row and top_k past 64
+    (300, 16, 2, 1024, 1), (129, 8, 3, 2048, 7), (64, 4, 2, 1056, 31), (33, 100, 70, 1024, 5),
+    (40, 8, 2, 4093, 3),
+])
+def test_permute_stable_offset_rows(ctx, device, tokens, experts, top_k, hidden, offset):
+    rng = np.random.default_rng(tokens + hidden + offset)
+    ids = np.stack([rng.permutation(experts)[:top_k] for _ in range(tokens)]).astype(np.int32)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    offsets, xp, pos, inv, cursors = run_permute(ctx, device, x, ids, experts, NATIVE, offset=offset)
+    e_pos = oracle.stable_route_pos(ids, offsets)
+    assert np.array_equal(pos, e_pos)
+    assert np.array_equal(inv, oracle.inverse_route(e_pos))
+    assert np.array_equal(xp.view(np.uint32), oracle.permute_rows(x, e_pos, top_k).view(np.uint32))
+    assert np.array_equal(cursors, np.diff(offsets))
+
+
 def test_permute_c4_skew_full_size(ctx, device):
     """C4 routing (Zipf 1.2 over 7 of 8 experts) at T=8192, K=4096: the map is
     bit-exact against the oracle and the copied rows are checked on the device
