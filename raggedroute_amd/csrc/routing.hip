@@ -882,16 +882,14 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
 
   constexpr int kChunk = 64 * kRowQuadsInFlight;  // quads per chunk
   f4u v[kRowQuadsInFlight];
+  // REALIGN == false: rows of whole quads (hidden % 32 == 0); a lane past the
+  // row's last quad loads that quad again (the top-2 copy stores it again, the
+  // same bytes to the same place; the other copy skips it)
   auto load_chunk = [&](const float* src, int q0) {
 #pragma unroll
     for (int u = 0; u < kRowQuadsInFlight; ++u) {
-      const int k0 = 4 * (q0 + lane + 64 * u);
-      if (k0 + 4 <= hidden) {
-        v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(src + k0));
-      } else {
-        v[u] = f4u{0.0F, 0.0F, 0.0F, 0.0F};
-        for (int e = 0; k0 + e < hidden; ++e) v[u][e] = src[k0 + e];
-      }
+      const int q = q0 + lane + 64 * u;
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(src + 4 * (q < cols ? q : cols - 1)));
     }
   };
   // REALIGN: quads [c0, c0 + kChunk) of the row's lines (nq quads from line0)
@@ -1101,6 +1099,58 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
     }
     return;
   }
+  if (top_k == 2) {
+    // Top-2 with every route of the wave's rows placed (one test per wave):
+    // the next chunk (this row's next or the wave's next row's first) is
+    // loaded before the current chunk's two stores, and every load and store
+    // is issued unconditionally (lanes past the row's last quad repeat that
+    // quad, the same bytes to the same place), so the compiler's wait before
+    // a chunk's stores leaves the previous chunk's stores in flight (C4,
+    // cold: 83.7 -> 82.3 us).
+    bool placed = true;
+    for (int t = t_first; t < t_end; t += kFusedWaves) {
+      placed = placed && slot[(t - t_begin) * 2] >= 0 && slot[(t - t_begin) * 2 + 1] >= 0;
+    }
+    if (__builtin_amdgcn_readfirstlane(placed ? 1 : 0) != 0) {
+      const int nchunks = (cols + kChunk - 1) / kChunk;
+      f4u w[kRowQuadsInFlight];
+      int t = t_first, c = 0;
+      while (t < t_end) {  // (wave-uniform)
+        const int32_t p0 = __builtin_amdgcn_readfirstlane(slot[(t - t_begin) * 2]);
+        const int32_t p1 = __builtin_amdgcn_readfirstlane(slot[(t - t_begin) * 2 + 1]);
+        int tn = t, cn = c + 1;
+        if (cn == nchunks) {
+          cn = 0;
+          tn = t + kFusedWaves;
+        }
+        if (tn < t_end) {
+          const float* nsrc = x + static_cast<std::size_t>(tn) * hidden;
+#pragma unroll
+          for (int u = 0; u < kRowQuadsInFlight; ++u) {
+            const int q = cn * kChunk + lane + 64 * u;
+            w[u] = __builtin_nontemporal_load(reinterpret_cast<const f4u*>(nsrc + 4 * (q < cols ? q : cols - 1)));
+          }
+        }
+        float* d0 = x_permuted + static_cast<std::size_t>(p0) * hidden;
+        float* d1 = x_permuted + static_cast<std::size_t>(p1) * hidden;
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) {
+          const int q = c * kChunk + lane + 64 * u;
+          __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(d0 + 4 * (q < cols ? q : cols - 1)));
+        }
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) {
+          const int q = c * kChunk + lane + 64 * u;
+          __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(d1 + 4 * (q < cols ? q : cols - 1)));
+        }
+#pragma unroll
+        for (int u = 0; u < kRowQuadsInFlight; ++u) v[u] = w[u];
+        t = tn;
+        c = cn;
+      }
+      return;
+    }
+  }
   for (int t = t_first; t < t_end; t += kFusedWaves) {
     const float* src = x + static_cast<std::size_t>(t) * hidden;
     const int32_t* my_slots = slot + (t - t_begin) * top_k;
@@ -1112,12 +1162,8 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
         float* dst = x_permuted + static_cast<std::size_t>(pos) * hidden;
 #pragma unroll
         for (int u = 0; u < kRowQuadsInFlight; ++u) {
-          const int k0 = 4 * (q0 + lane + 64 * u);
-          if (k0 + 4 <= hidden) {
-            __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(dst + k0));
-          } else {
-            for (int e = 0; k0 + e < hidden; ++e) dst[k0 + e] = v[u][e];
-          }
+          const int q = q0 + lane + 64 * u;
+          if (q < cols) __builtin_nontemporal_store(v[u], reinterpret_cast<f4u*>(dst + 4 * q));
         }
       }
     }

@@ -391,6 +391,9 @@ def test_permute_unaligned_duplicate_ids(ctx, device, kat, kernel):
     # ... destination rows at every 16-byte phase across chunk boundaries
     # (a chunk is 2048 floats: the realigned quads take the next chunk's first)
     (700, 16, 2, 2049), (300, 8, 2, 4097), (257, 8, 2, 6143),
+    # ... top-2 rows on 128-byte lines (the pipelined copy): a row shorter than
+    # one chunk, a second chunk of 8 quads, several rows per wave
+    (3000, 16, 2, 1024), (900, 8, 2, 2080), (5000, 64, 2, 1536),
 ])
 def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     rng = np.random.default_rng(tokens + experts)
