@@ -430,6 +430,51 @@ def test_permute_stable_offset_rows(ctx, device, tokens, experts, top_k, hidden,
     assert np.array_equal(cursors, np.diff(offsets))
 
 
+@pytest.mark.parametrize("tokens,experts,hidden", [(600, 8, 1024), (600, 8, 1100), (90, 4, 4096)])
+def test_permute_wide_rows_invalid_ids(ctx, device, tokens, experts, hidden):
+    """Wide top-2 rows with a few route ids outside [0, E): those routes map to
+    -1 and their rows are not copied (the wave holding such a route takes the
+    general copy loop); every other route keeps its stable position. Offsets
+    count the valid ids only. The expected map is computed here in numpy: the
+    oracle rejects invalid ids, as the reference's does."""
+    rng = np.random.default_rng(tokens + hidden)
+    ids = np.stack([rng.permutation(experts)[:2] for _ in range(tokens)]).astype(np.int32).reshape(-1)
+    bad = rng.choice(ids.size, 7, replace=False)
+    ids[bad[:4]] = -1
+    ids[bad[4:]] = experts
+    valid = (ids >= 0) & (ids < experts)
+    counts = np.bincount(ids[valid], minlength=experts).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    e_pos = np.full(ids.size, -1, np.int32)
+    cursor = offsets[:-1].copy()
+    for r in range(ids.size):
+        if valid[r]:
+            e_pos[r] = cursor[ids[r]]
+            cursor[ids[r]] += 1
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    routes = 2 * tokens
+    xd = to_dev(x, device)
+    xp = torch.full((routes, hidden), float("nan"), dtype=torch.float32, device=device)
+    ids_d = to_dev(ids, device)
+    offs_d = to_dev(offsets, device)
+    pos = torch.full((routes,), -5, dtype=torch.int32, device=device)
+    cursors = torch.full((experts,), 99, dtype=torch.int32, device=device)
+    args = rr.TokenPermuteArgs(x=rr.cview(p(xd)), expert_ids=p(ids_d), offsets=p(offs_d),
+                               x_permuted=rr.mview(p(xp)), route_pos=p(pos), tokens=tokens,
+                               experts=experts, top_k=2, hidden=hidden, kernel=NATIVE)
+    pctx = rr.RuntimeContext(stream=ctx.stream, workspace=p(cursors), workspace_bytes=experts * 4,
+                             architecture=ctx.architecture)
+    ok(rr.token_permute(args, pctx))
+    assert np.array_equal(to_host(pos), e_pos)
+    got = to_host(xp)
+    filled = np.zeros(routes, bool)
+    filled[e_pos[valid]] = True
+    expect = x[np.nonzero(valid)[0][np.argsort(e_pos[valid])] // 2]
+    assert np.array_equal(got[filled].view(np.uint32), expect.view(np.uint32))
+    assert np.isnan(got[~filled]).all()
+    assert np.array_equal(to_host(cursors), counts)
+
+
 def test_permute_c4_skew_full_size(ctx, device):
     """C4 routing (Zipf 1.2 over 7 of 8 experts) at T=8192, K=4096: the map is
     bit-exact against the oracle and the copied rows are checked on the device
