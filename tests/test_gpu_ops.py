@@ -328,6 +328,78 @@ def test_histogram_large_hot_expert(ctx, guarded, experts, share, offset):
         assert counts.canaries_intact() and offsets.canaries_intact() and ids.canaries_intact()
 
 
+def _hist_case(routes, experts, seed, device):
+    rng = np.random.default_rng(seed)
+    ids_h = rng.integers(0, experts, routes).astype(np.int32)
+    ids_h[rng.random(routes) < 0.3] = int(rng.integers(0, experts))
+    e_c = np.bincount(ids_h, minlength=experts).astype(np.int32)
+    e_o = np.concatenate([[0], np.cumsum(e_c)]).astype(np.int32)
+    ids = to_dev(ids_h, device)
+    counts = torch.full((experts,), 77, dtype=torch.int32, device=device)
+    offsets = torch.full((experts + 1,), -9, dtype=torch.int32, device=device)
+    return ids, counts, offsets, e_c, e_o
+
+
+def _hist_call(ids, counts, offsets, routes, experts, stream, fused=True):
+    cx = rr.RuntimeContext(stream=stream, architecture=int(rr.DeviceArchitecture.kGfx950))
+    if fused:
+        ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
+            expert_ids=p(ids), counts=p(counts), offsets=p(offsets), route_pairs=routes,
+            experts=experts, kernel=NATIVE), cx))
+    else:
+        ok(rr.histogram(rr.HistogramArgs(expert_ids=p(ids), counts=p(counts), route_pairs=routes,
+                                         experts=experts, kernel=NATIVE), cx))
+
+
+def test_histogram_large_streams(device):
+    """Large R on twenty streams, each with its own ids, enqueued without waits
+    between them so the calls overlap; twice; both the fused and the
+    counts-only operator (each call's counts and ticket live in its own
+    buffers, so concurrent calls never share state)."""
+    routes, experts = 200003, 33
+    streams = [torch.cuda.Stream(device) for _ in range(20)]
+    cases = [_hist_case(routes, experts, 100 + i, device) for i in range(len(streams))]
+    torch.cuda.synchronize()
+    for rnd in range(2):
+        for (ids, counts, offsets, _, _), s in zip(cases, streams):
+            counts.fill_(77)
+            offsets.fill_(-9)
+        torch.cuda.synchronize()
+        for i, ((ids, counts, offsets, _, _), s) in enumerate(zip(cases, streams)):
+            _hist_call(ids, counts, offsets, routes, experts, s.cuda_stream, fused=(i + rnd) % 3 != 0)
+        torch.cuda.synchronize()
+        for i, (ids, counts, offsets, e_c, e_o) in enumerate(cases):
+            assert np.array_equal(to_host(counts), e_c), (rnd, i)
+            if (i + rnd) % 3 != 0:
+                assert np.array_equal(to_host(offsets), e_o), (rnd, i)
+
+
+def test_histogram_large_graph_replays(device):
+    """Large R captured in a graph (zeroing kernel and counting kernel, no
+    memset node), replayed three times with eager calls of other ids on the
+    same stream between the replays; every replay and every eager call exact."""
+    routes, experts = 300007, 256
+    ids, counts, offsets, e_c, e_o = _hist_case(routes, experts, 7, device)
+    ids2, counts2, offsets2, e_c2, e_o2 = _hist_case(routes, experts, 8, device)
+    stream = torch.cuda.Stream(device)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        _hist_call(ids, counts, offsets, routes, experts, stream.cuda_stream)
+    for _ in range(3):
+        counts.fill_(77)
+        offsets.fill_(-9)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(counts), e_c) and np.array_equal(to_host(offsets), e_o)
+        _hist_call(ids2, counts2, offsets2, routes, experts, stream.cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(counts2), e_c2) and np.array_equal(to_host(offsets2), e_o2)
+    del graph
+
+
 # -------------------------------------------------------------------- permute
 
 def run_permute(ctx, device, x_h, ids_h, experts, kernel, with_inverse=True, offset=0):
