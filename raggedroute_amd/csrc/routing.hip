@@ -1113,7 +1113,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
     }
     if (__builtin_amdgcn_readfirstlane(placed ? 1 : 0) != 0) {
       const int nchunks = (cols + kChunk - 1) / kChunk;
-      f4u w[kRowQuadsInFlight];
+      f4u w[kRowQuadsInFlight] = {};  // (the last step loads nothing)
       int t = t_first, c = 0;
       while (t < t_end) {  // (wave-uniform)
         const int32_t p0 = __builtin_amdgcn_readfirstlane(slot[(t - t_begin) * 2]);
