@@ -466,6 +466,10 @@ def test_permute_unaligned_duplicate_ids(ctx, device, kat, kernel):
     # ... top-2 rows on 128-byte lines (the pipelined copy): a row shorter than
     # one chunk, a second chunk of 8 quads, several rows per wave
     (3000, 16, 2, 1024), (900, 8, 2, 2080), (5000, 64, 2, 1536),
+    # ... realigned rows whose source fits one chunk while a destination's
+    # phase needs a second (the chunk prefetched before the ranks is then not
+    # the one the copy wants next)
+    (300, 16, 2, 2041), (257, 8, 2, 2030),
 ])
 def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     rng = np.random.default_rng(tokens + experts)
