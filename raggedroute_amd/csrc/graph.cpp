@@ -13,12 +13,16 @@
 //
 // On ROCm 7.2 one hipGraphLaunch has a fixed cost (measured on MI355X: about
 // 19 us of host time and 5 us of GPU time before the first node) that a graph
-// of one headline chain (two kernels, ~23 us) does not win back; a sequence
+// of one headline chain (two kernels, ~20 us) does not win back; a sequence
 // of ten or more chains per graph runs at the direct calls' GPU time with a
-// fraction of their host submission time.
+// fraction of their host submission time. A graph of at most kDirectCalls
+// chains is therefore replayed by launching its recorded kernel nodes one by
+// one (same kernels, grids and argument values, in capture order) instead of
+// through hipGraphLaunch (RR_CHAIN_GRAPH_DIRECT=off keeps hipGraphLaunch).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -31,6 +35,9 @@ struct rr_chain_graph {
   int32_t entry = 0;
   int32_t calls = 1;  // chain calls recorded, in order
   int32_t kernel_nodes = 0;
+  // short sequences: the kernel nodes in launch order, replayed directly
+  // (their argument buffers belong to `graph`); empty: hipGraphLaunch
+  std::vector<hipKernelNodeParams> direct;
 };
 
 namespace rr {
@@ -123,6 +130,46 @@ int32_t count_kernel_nodes(hipGraph_t graph) noexcept {
   return kernels;
 }
 
+constexpr int32_t kDirectCalls = 2;
+
+bool direct_allowed() noexcept {
+  static const bool allowed = [] {
+    const char* v = std::getenv("RR_CHAIN_GRAPH_DIRECT");
+    return v == nullptr || std::strcmp(v, "off") != 0;
+  }();
+  return allowed;
+}
+
+// The kernel nodes of a captured single-stream sequence in launch order: one
+// root, each node with at most one dependent, every node a kernel node. Any
+// other shape leaves `out` empty (the graph is then replayed by hipGraphLaunch).
+void collect_direct(hipGraph_t graph, std::vector<hipKernelNodeParams>* out) noexcept {
+  out->clear();
+  size_t total = 0;
+  size_t roots = 0;
+  if (hipGraphGetNodes(graph, nullptr, &total) != hipSuccess || total == 0) return;
+  if (hipGraphGetRootNodes(graph, nullptr, &roots) != hipSuccess || roots != 1) return;
+  hipGraphNode_t node = nullptr;
+  if (hipGraphGetRootNodes(graph, &node, &roots) != hipSuccess) return;
+  std::vector<hipKernelNodeParams> order;
+  while (node != nullptr && order.size() < total) {
+    hipGraphNodeType type{};
+    hipKernelNodeParams p{};
+    if (hipGraphNodeGetType(node, &type) != hipSuccess || type != hipGraphNodeTypeKernel ||
+        hipGraphKernelNodeGetParams(node, &p) != hipSuccess || p.extra != nullptr) {
+      return;
+    }
+    order.push_back(p);
+    size_t deps = 0;
+    if (hipGraphNodeGetDependentNodes(node, nullptr, &deps) != hipSuccess || deps > 1) return;
+    hipGraphNode_t next = nullptr;
+    if (deps == 1 && hipGraphNodeGetDependentNodes(node, &next, &deps) != hipSuccess) return;
+    node = deps == 1 ? next : nullptr;
+  }
+  if (node != nullptr || order.size() != total) return;
+  *out = std::move(order);
+}
+
 rr_status instantiate(rr_chain_graph* g, hipStream_t stream) noexcept {
   hipError_t err = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
   if (err != hipSuccess) {
@@ -160,6 +207,7 @@ rr_status create(int32_t entry, const void* const* args, int32_t count,
     return status;
   }
   g->kernel_nodes = count_kernel_nodes(g->graph);
+  if (count <= kDirectCalls && direct_allowed()) collect_direct(g->graph, &g->direct);
   *out = g;
   return ok_status();
 }
@@ -179,9 +227,11 @@ rr_status update(rr_chain_graph* g, const void* const* args, int32_t count,
   hipGraphNode_t error_node = nullptr;
   hipGraphExecUpdateResult result = hipGraphExecUpdateError;
   const hipError_t err = hipGraphExecUpdate(g->exec, fresh, &error_node, &result);
+  g->direct.clear();  // (its argument buffers belong to the graph destroyed here)
   (void)hipGraphDestroy(g->graph);
   g->graph = fresh;
   g->kernel_nodes = count_kernel_nodes(fresh);
+  if (count <= kDirectCalls && direct_allowed()) collect_direct(fresh, &g->direct);
   if (err == hipSuccess && result == hipGraphExecUpdateSuccess) return ok_status();
   (void)hipGetLastError();  // a rejected update is not a device error
   (void)hipGraphExecDestroy(g->exec);
@@ -264,6 +314,13 @@ rr_status rr_chain_graph_create_sequence(int32_t entry, const void* const* args,
 
 rr_status rr_chain_graph_launch(rr_chain_graph* graph, hipStream_t stream) {
   if (graph == nullptr || graph->exec == nullptr) return rr::invalid_argument("chain graph must not be null");
+  if (!graph->direct.empty()) {
+    for (const hipKernelNodeParams& p : graph->direct) {
+      const hipError_t err = hipLaunchKernel(p.func, p.gridDim, p.blockDim, p.kernelParams, p.sharedMemBytes, stream);
+      if (err != hipSuccess) return rr::device_status(err, "chain graph launch failed");
+    }
+    return rr::ok_status();
+  }
   return rr::device_status(hipGraphLaunch(graph->exec, stream), "chain graph launch failed");
 }
 
