@@ -229,6 +229,22 @@ class Chain:
             raise RuntimeError(f"{name}: {status.message}")
 
 
+def settle(torch, fn, busy_s=0.03, probe=10):
+    """Untimed back-to-back calls of `fn` until the GPU has run them for about
+    `busy_s` (the per-call time from `probe` calls): launches reach their
+    steady-state rate only after about 20 ms of continuous load (see
+    SETTLE_CHAINS)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(probe):
+        fn()
+    torch.cuda.synchronize()
+    per = max((time.perf_counter() - t0) / probe, 1e-6)
+    for _ in range(int(busy_s / per)):
+        fn()
+    torch.cuda.synchronize()
+
+
 def time_loop(torch, fn, reps, warmup=3):
     """Average seconds per call of `fn` over `reps` back-to-back launches,
     bracketed by HIP events on the current stream (host-submitted: use for
@@ -288,7 +304,13 @@ def sample_stats(seconds):
 
 
 MIN_BATCH = 10      # chains per timed sample (the reference runner's kernel_repeats role)
-SETTLE_CHAINS = 50  # untimed chains before the first sample, counting --warmup
+# Untimed back-to-back chains before the first timed sample, counting
+# --warmup, and again before the per-launch and per-stage timings. The chain
+# reaches its steady state only after about 20 ms of continuous load (measured
+# on MI355X, p50 of 20 batches of 10 after N chains: N = 50 20.2-20.4 us, 200
+# 20.0, 500 19.6, 1000 19.3, 2000-8000 19.3; after 0.5 s idle, 50 chains give
+# 20.4 us again).
+SETTLE_CHAINS = 1500
 
 
 def batch_sizes(steps, samples=20, min_batch=MIN_BATCH):
@@ -389,7 +411,8 @@ def graph_report(torch, device, ch, reps=200):
     direct calls: GPU time per chain (events over back-to-back launches on one
     stream) and host time to submit one chain (no synchronisation inside the
     loop), for graphs of 1, 10 and 50 chains (a sequence graph: one
-    hipGraphLaunch replays them all)."""
+    hipGraphLaunch replays them all). Each form is first settled (settle) so
+    that all of them are timed at the steady-state clock."""
     rr = ch.rr
     stream = torch.cuda.Stream(device)
     ctx = ch.ctx_on(stream.cuda_stream)
@@ -411,6 +434,7 @@ def graph_report(torch, device, ch, reps=200):
 
     out = {}
     with torch.cuda.stream(stream):
+        settle(torch, direct)
         out["direct_us"] = round(time_loop(torch, direct, reps, warmup=10) * 1e6, 2)
         out["direct_submit_us"] = submit_us(direct, 1, reps)
         for chains in (1, 10, 50):
@@ -420,6 +444,7 @@ def graph_report(torch, device, ch, reps=200):
                     assert status.ok(), status.message
                 n = max(4, reps // chains)
                 key = f"graph{chains}"
+                settle(torch, replay, probe=3)
                 out[f"{key}_kernel_nodes"] = graph.kernel_nodes
                 out[f"{key}_us"] = round(time_loop(torch, replay, n, warmup=3) * 1e6 / chains, 2)
                 out[f"{key}_submit_us"] = submit_us(replay, chains, n)
@@ -453,8 +478,8 @@ def launch_report(torch, device, ch, model, n=50):
 
 def headline(torch, device, args):
     """The headline chain: `--warmup` untimed chains (then more untimed chains
-    up to SETTLE_CHAINS in all: the clock needs about 50 back-to-back chains
-    to settle), then exactly `--steps` chains in batches of at least
+    up to SETTLE_CHAINS in all: the chain reaches its steady state after about
+    20 ms of back-to-back chains), then exactly `--steps` chains in batches of at least
     MIN_BATCH (reference runner: each sample is the event span of a batch
     divided by its size); value = T / p50 of the batch means. The outputs of
     the last timed chain are copied to the host for validation. Then the cold
@@ -482,6 +507,9 @@ def headline(torch, device, args):
     mean_s = sum(m * n for m, n in zip(means, sizes)) / args.steps
     cold = sample_stats(cold_spans(torch, ch, device, samples=20))
     active = int((ch.counts.cpu().numpy() > 0).sum())
+    for _ in range(SETTLE_CHAINS):  # (the cold samples let the clock drop)
+        ch.chain()
+    torch.cuda.synchronize()
     launches = launch_report(torch, device, ch,
                              fused_work_model(cfg.tokens, cfg.experts, cfg.hidden, cfg.output, active))
     ch.chain()  # restore y (timing the last launch alone keeps adding into it)
@@ -523,7 +551,7 @@ def c4(torch, device, hidden=4096, output=14336, reps=5, samples=10, cpu_sample=
     for name in ("token_permute", "grouped_gemm", "unpermute"):
         nbytes, flops = model[name]
         if name == "grouped_gemm":
-            sec = time_loop(torch, lambda: ch.stage(name), reps, warmup=1)
+            sec = time_loop(torch, lambda: ch.stage(name), reps, warmup=2)  # (two calls: ~30 ms of load)
             out[name] = {"us": round(sec * 1e6, 1), "roofline": roofline(name, nbytes, flops, sec)}
             continue
         warm = statistics.median(batch_means(torch, lambda: ch.stage(name), samples=samples, repeats=5))
@@ -545,6 +573,7 @@ def c5(torch, device, steps=20, cpu_sample=False):
     cfg = workloads.C5
     inputs = workloads.chain_inputs_device(cfg, 0, device)
     ch = Chain(cfg, inputs, device)
+    settle(torch, ch.chain, probe=3)
     sec = time_loop(torch, ch.chain, steps, warmup=3)
     active = int((ch.counts.cpu().numpy() > 0).sum())
     launches = launch_report(torch, device, ch,
@@ -614,6 +643,7 @@ def small_chain(torch, device, cfg, reps=200):
     inputs = workloads.chain_inputs(cfg, 0)
     dev_inputs = {k: torch.from_numpy(v).to(device) for k, v in inputs.items()}
     ch = Chain(cfg, dev_inputs, device)
+    settle(torch, ch.chain)
     sec = time_loop(torch, ch.chain, reps, warmup=10)
     stats = sample_stats(batch_means(torch, ch.chain, samples=20, repeats=10))
     del ch, dev_inputs
@@ -653,6 +683,7 @@ def route_chain(torch, device, reps=200):
         def call():
             status = rr.chain_from_route_ids(args, ctx)
             assert status.ok(), status.message
+        settle(torch, call)
         sec = time_loop(torch, call, reps, warmup=10)
         out[name] = {"T": t, "E": e, "K": k, "N": n, "top_k": top, "us": round(sec * 1e6, 2),
                      "tokens_per_s": round(t / sec, 1),
@@ -875,9 +906,9 @@ def profile(torch, device, case):
     if case == "headline":
         cfg = workloads.HEADLINE
         ch = Chain(cfg, workloads.chain_inputs_device(cfg, 0, device), device)
-        # (enough back-to-back calls for the clocks to settle: the later
-        # dispatches of each kernel are the steady state)
-        for _ in range(50):
+        # SETTLE_CHAINS untimed chains bring the chain to its steady state;
+        # the 50 chains after them are the ones the summary reads
+        for _ in range(SETTLE_CHAINS + 50):
             ch.chain()
         torch.cuda.synchronize()
         for index in range(len(ch.rr.chain_fused_launch_names(ch.chain_args, cfg.from_tokens))):
@@ -887,7 +918,7 @@ def profile(torch, device, case):
             for _ in range(20):
                 ch.stage(name)
         torch.cuda.synchronize()
-        print("profile: headline done (50 chains, 20 x each fused launch, 20 x each stage)", flush=True)
+        print(f"profile: headline done ({SETTLE_CHAINS} + 50 chains, 20 x each fused launch, 20 x each stage)", flush=True)
     elif case == "c4":
         c4(torch, device, reps=2, samples=3)
         print("profile: c4 (K 4096, N 14336) done", flush=True)
@@ -922,7 +953,7 @@ STAMP_PHASES = [   # (slot, phase ending at that stamp)
     (10, "route map, rest of B issued")]
 
 
-def phase_stamps(torch, device, chains=80, out=""):
+def phase_stamps(torch, device, chains=SETTLE_CHAINS, out=""):
     """Phase times of the headline chain's expert launch (the merged route
     preparation + expert GEMM + combine) from the instrumentation build, whose
     strip kernel writes the shader clock at each phase boundary of every wave
