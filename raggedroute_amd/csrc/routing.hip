@@ -855,6 +855,20 @@ constexpr int kRealignPad = 8;                                                  
 constexpr int kRealignStripQuads = 64 * kRowQuadsInFlight + 2 * kRealignPad;  // per wave
 typedef float f4a __attribute__((ext_vector_type(4)));                         // 16-byte aligned
 
+// Chunks per realigned row. A row's last float lies in source quad
+// (hidden - 1 + hs) / 4 of its lines and in destination quad (hidden - 1 +
+// hd) / 4, both at most (hidden + 30) / 4 for phases below 32 floats. A
+// chunk's strip holds source quads up to c0 + kChunk + kRealignPad - 1, and
+// its last step lets lanes 0..kRealignPad-1 write destination quads c0 +
+// kChunk .. + kRealignPad - 1 from it, so the row takes the fewest chunks
+// whose last strip reaches that quad: two at K = 4095, where counting every
+// destination's quads alone (up to 1025) would take a third chunk for one quad.
+__host__ __device__ inline int realign_chunks(int hidden) {
+  const int last_q = (hidden + 30) >> 2;
+  const int n = (last_q - kRealignPad + 64 * kRowQuadsInFlight) / (64 * kRowQuadsInFlight);
+  return n > 1 ? n : 1;
+}
+
 __host__ __device__ inline int realign_strip_offset(int experts, int tokens_per_block, int top_k) {
   // int32 offset of the realign strips in the block's LDS, 16-byte aligned
   return ((kFusedWaves + 1) * experts + tokens_per_block * top_k + 3) & ~3;
@@ -940,8 +954,8 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
         const int q = kChunk + lane - kRealignPad;
         __builtin_amdgcn_global_load_lds(l0 + 4 * (q < nq ? q : nq - 1), strip0 + 4 * kChunk, 16, 0, 2 /* nt */);
       }
-      pre_t = nq > kChunk ? t_first : t_first + kFusedWaves;
-      pre_c = nq > kChunk ? kChunk : 0;
+      pre_t = realign_chunks(hidden) > 1 ? t_first : t_first + kFusedWaves;
+      pre_c = realign_chunks(hidden) > 1 ? kChunk : 0;
       if (pre_t < t_end) {
         const float* ps = x + static_cast<std::size_t>(pre_t) * hidden;
         const int hp = row_phase(ps);
@@ -1083,27 +1097,16 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
     // Once a chunk sits in the strip its registers are free: the next chunk's
     // loads (this row's next or the wave's next row's first) are issued before
     // the current chunk's stores, so their latency runs under the stores.
-    auto span_of = [&](int t, int nq) {  // quads to cover: the source's and every destination's
-      const int32_t* my_slots = slot + (t - t_begin) * top_k;
-      int span = nq;
-      for (int j = 0; j < top_k; ++j) {
-        const int32_t pos = my_slots[j];
-        if (pos >= 0) {
-          const int nd = (hidden + row_phase(x_permuted + static_cast<std::size_t>(pos) * hidden) + 3) >> 2;
-          span = nd > span ? nd : span;
-        }
-      }
-      return span;
-    };
+    const int nch = realign_chunks(hidden);
     for (int t = t_first; t < t_end; t += kFusedWaves) {
       const float* src = x + static_cast<std::size_t>(t) * hidden;
       const int hs = row_phase(src);
       const f4a* line0 = reinterpret_cast<const f4a*>(src - hs);
       const int nq = (hidden + hs + 3) >> 2;
       const int32_t* my_slots = slot + (t - t_begin) * top_k;
-      const int span = span_of(t, nq);
-      for (int c0 = 0; c0 < span; c0 += kChunk) {
-        const bool first = t == t_first && c0 == 0;  // (in the strip since before the rank phase)
+      for (int c = 0; c < nch; ++c) {
+        const int c0 = c * kChunk;
+        const bool first = t == t_first && c == 0;  // (in the strip since before the rank phase)
         if (first) {
           __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed
         } else {
@@ -1116,7 +1119,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
         }
         wave_lds_sync();
         if (!first) {
-          if (c0 + kChunk < span) {
+          if (c + 1 < nch) {
             load_lines(line0, nq, c0 + kChunk);
             pre_t = t;
             pre_c = c0 + kChunk;
@@ -1149,6 +1152,22 @@ __global__ __launch_bounds__(kFusedWaves * 64) void rr_permute_rank_rows_kernel(
                 for (int e = 0; e < 4; ++e) {
                   if (f0 + e >= 0 && f0 + e < hidden) dst[f0 + e] = o[e];
                 }
+              }
+            }
+          }
+          if (c + 1 == nch && lane < kRealignPad) {
+            // the row's last destination quads, past the chunk: each float of
+            // the row (below hidden) lies in the strip (realign_chunks); the
+            // others are neither read nor stored
+            const int i = c0 + kChunk + lane;
+            if (i < nd) {
+              const int off = 4 * (kRealignPad + kChunk + lane) + hs - hd;
+              const int f0 = 4 * i - hd;
+              if (f0 + 4 <= hidden) {
+                const f4a o = f4a{strip_f[off], strip_f[off + 1], strip_f[off + 2], strip_f[off + 3]};
+                __builtin_nontemporal_store(o, reinterpret_cast<f4a*>(dline + 4 * i));
+              } else {
+                for (int e = 0; f0 + e < hidden; ++e) dst[f0 + e] = strip_f[off + e];
               }
             }
           }

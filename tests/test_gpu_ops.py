@@ -493,6 +493,11 @@ def test_permute_stable_bit_exact(ctx, device, tokens, experts, top_k, hidden):
     # line-realigned path; with a tail, a 2-chunk row and top_k past 64
     (300, 16, 2, 1024, 1), (129, 8, 3, 2048, 7), (64, 4, 2, 1056, 31), (33, 100, 70, 1024, 5),
     (40, 8, 2, 4093, 3),
+    # widths at the chunk-count boundaries of the realigned copy: 2049 floats
+    # is the widest one-chunk row (its last quads written by the tail lanes),
+    # 2050 takes two chunks, 4095 and 4097 two (the tail lanes again), 4098 three
+    (50, 8, 2, 2049, 0), (50, 8, 2, 2050, 1), (37, 8, 2, 4095, 0), (30, 8, 2, 4097, 3),
+    (20, 4, 3, 4098, 0),
 ])
 def test_permute_stable_offset_rows(ctx, device, tokens, experts, top_k, hidden, offset):
     rng = np.random.default_rng(tokens + hidden + offset)
