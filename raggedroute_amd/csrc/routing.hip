@@ -221,7 +221,7 @@ std::size_t bins_bytes(int experts) {
 }
 
 // ---- large R: LDS histograms per block, device atomics, last-block scan ----
-// 256 threads, 32 ids per thread per pass (eight 16-byte loads issued before
+// 512 threads, 16 ids per thread per pass (four 16-byte loads issued before
 // any is used), one LDS row per wave, one direct ds_add per id. A wave whose
 // first 64 ids show a dominant expert (one of four probed lanes' ids held by
 // at least 12 of them) counts that expert with a ballot per load instead: its
@@ -229,9 +229,12 @@ std::size_t bins_bytes(int experts) {
 // lanes on one address) and their popcounts are summed in a scalar register.
 // At R = 2^20 (warm, E = 33 / 256): hot50 9.98 / 10.83 -> 8.1 / 8.8 us,
 // uniform 7.73 / 8.51 -> 7.6 / 8.4 us (the ballot loop is a separate copy of
-// the id loop: a per-id test in one loop cost uniform 0.8 us).
-constexpr int kHistThreads = 256;
-constexpr int kHistIds = 32;
+// the id loop: a per-id test in one loop cost uniform 0.8 us). Eight waves of
+// 16 ids instead of four of 32 (same 8192 ids per block): uniform 7.62 / 8.50
+// -> 7.30 / 8.05 us, hot50 8.16 / 8.90 -> 7.95 / 8.79 (two interleaved runs;
+// sixteen waves of 8 ids measured the same as eight).
+constexpr int kHistThreads = 512;
+constexpr int kHistIds = 16;
 constexpr int kHistPass = kHistThreads * kHistIds;  // ids per block per pass
 
 // counts[0, experts) = 0, and with offsets given offsets[experts] = 0 (the
@@ -260,7 +263,7 @@ template <bool VEC>
 __global__ __launch_bounds__(kHistThreads) void rr_hist_atomic_kernel(
     const int32_t* __restrict__ ids, int32_t* counts, int32_t* offsets, int routes, int experts,
     int chunk) {
-  extern __shared__ int32_t lds[];  // [4][experts] rows
+  extern __shared__ int32_t lds[];  // [waves][experts] rows
   __shared__ int s_last;
   constexpr int kWaves = kHistThreads / 64;
   const int tid = static_cast<int>(threadIdx.x);
@@ -383,7 +386,10 @@ hipError_t histogram_atomic(const int32_t* ids, int32_t* counts, int32_t* offset
   // Every block adds its nonzero bins into the global counts, so each count
   // takes one atomic per block, serialised at the memory side: at R = 2^20,
   // 128 blocks measured 8.8 / 9.2 us (E = 33 / 256) against 9.4 / 11.1 with
-  // 256 and 11.1 / 11.6 with 32 (fewer blocks crowd the hot-expert bins).
+  // 256 and 11.1 / 11.6 with 32 (fewer blocks crowd the hot-expert bins); with
+  // 512-thread blocks 7.3 / 8.1 against 8.6 / 10.1 with 256 blocks and 7.4 /
+  // 7.7 with 64, whose hot50 cases then lose 1 / 0.4 us. Two bins per 64-bit
+  // atomic (half the atomics) was slower: 7.3 / 8.0 -> 8.0 / 8.6 us.
   const long passes = (static_cast<long>(routes) + kHistPass - 1) / kHistPass;
   long blocks = passes < 128 ? passes : 128;
   const long by_experts = static_cast<long>(routes) / (8L * experts);  // >= 8 ids per global add
@@ -391,7 +397,7 @@ hipError_t histogram_atomic(const int32_t* ids, int32_t* counts, int32_t* offset
   const long per_block = (passes + blocks - 1) / blocks;
   const int chunk = static_cast<int>(per_block * kHistPass);
   blocks = (routes + static_cast<long>(chunk) - 1) / chunk;
-  const std::size_t lds = 4 * static_cast<std::size_t>(experts) * sizeof(int32_t);
+  const std::size_t lds = (kHistThreads / 64) * static_cast<std::size_t>(experts) * sizeof(int32_t);
   if (aligned16(ids)) {
     rr_hist_atomic_kernel<true><<<static_cast<unsigned>(blocks), kHistThreads, lds, stream>>>(
         ids, counts, offsets, routes, experts, chunk);

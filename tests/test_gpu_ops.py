@@ -275,7 +275,7 @@ def test_histogram_large_paths(ctx, guarded, routes, experts, offset):
     """Multi-block path (R > 65536): ragged end, unaligned ids (scalar loads),
     E = 1024 (several passes per block), out-of-range ids skipped, and two calls
     in a row on the same buffers (the last-block ticket starts from zero each
-    call)."""
+    call). Counts sit `offset` elements past an aligned base too."""
     rng = np.random.default_rng(routes + experts)
     ids_h = rng.integers(0, experts, routes).astype(np.int32)
     ids_h[rng.integers(0, routes, 50)] = -3
@@ -285,7 +285,7 @@ def test_histogram_large_paths(ctx, guarded, routes, experts, offset):
     e_o = np.concatenate([[0], np.cumsum(e_c)]).astype(np.int32)
     ids = guarded(routes, np.int32, ids_h, offset_elems=offset)
     for _ in range(2):
-        counts = guarded(experts, np.int32, np.full(experts, 123, np.int32))
+        counts = guarded(experts, np.int32, np.full(experts, 123, np.int32), offset_elems=offset)
         offsets = guarded(experts + 1, np.int32, np.full(experts + 1, 456, np.int32))
         ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
             expert_ids=ids.ptr, counts=counts.ptr, offsets=offsets.ptr, route_pairs=routes,
@@ -316,7 +316,7 @@ def test_histogram_large_hot_expert(ctx, guarded, experts, share, offset):
     e_o = np.concatenate([[0], np.cumsum(e_c)]).astype(np.int32)
     ids = guarded(routes, np.int32, ids_h, offset_elems=offset)
     for _ in range(2):
-        counts = guarded(experts, np.int32, np.full(experts, 77, np.int32))
+        counts = guarded(experts, np.int32, np.full(experts, 77, np.int32), offset_elems=offset)
         offsets = guarded(experts + 1, np.int32, np.full(experts + 1, -9, np.int32))
         ok(rr.histogram_exclusive_scan(rr.HistogramExclusiveScanArgs(
             expert_ids=ids.ptr, counts=counts.ptr, offsets=offsets.ptr, route_pairs=routes,
