@@ -232,7 +232,9 @@ std::size_t bins_bytes(int experts) {
 // the id loop: a per-id test in one loop cost uniform 0.8 us). Eight waves of
 // 16 ids instead of four of 32 (same 8192 ids per block): uniform 7.62 / 8.50
 // -> 7.30 / 8.05 us, hot50 8.16 / 8.90 -> 7.95 / 8.79 (two interleaved runs;
-// sixteen waves of 8 ids measured the same as eight).
+// sixteen waves of 8 ids measured the same as eight). Probing 8 or 16 lanes
+// for the hot expert instead of 4 made every case slower (E33 uniform 7.25 ->
+// 7.41 / 7.74 us, hot50 7.95 -> 8.10 / 8.37).
 constexpr int kHistThreads = 512;
 constexpr int kHistIds = 16;
 constexpr int kHistPass = kHistThreads * kHistIds;  // ids per block per pass
